@@ -1,0 +1,481 @@
+// capi.hip -- the C ABI (include/megamoe_hip.h): validation, workspace layout, schedule choice
+// and the stream-ordered launch sequence of the layer. No allocation, no host synchronisation.
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <atomic>
+
+#include "../../include/megamoe_hip.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int kTokenAlignment = 384;  // deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:9
+constexpr int kMaxTopk = 16;
+constexpr int kDefaultThreshold = 128;  // megamoe/__init__.py:22
+
+int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+int check_common(int num_ranks, int num_experts, int num_max_tokens, int num_topk, int hidden,
+                 int intermediate) {
+  if (num_ranks <= 0) return MMOE_ERR_NUM_RANKS;
+  if (num_experts % num_ranks != 0) return MMOE_ERR_EXPERTS_DIVISIBLE;
+  if (hidden <= 0 || intermediate <= 0) return MMOE_ERR_HIDDEN_SIZES;
+  if (num_max_tokens < 0) return MMOE_ERR_ARGUMENT;
+  if (num_topk <= 0 || num_topk > kMaxTopk) return MMOE_ERR_TOPK;
+  if (num_experts / num_ranks <= 0 || num_experts / num_ranks > mmoe::kMaxExperts)
+    return MMOE_ERR_UNSUPPORTED_SHAPE;
+  return MMOE_OK;
+}
+
+void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_topk, int hidden,
+                  int intermediate, mmoe_scratch_layout* l) {
+  const int64_t e_local = num_experts / num_ranks;
+  const int64_t tasks = static_cast<int64_t>(num_max_tokens) * num_topk;
+  const int64_t rows = align_up(tasks > 0 ? tasks : 1, 256);
+  const int64_t chunks = (tasks + mmoe::kRouteChunk - 1) / mmoe::kRouteChunk;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = off;
+    off = align_up(off + bytes, 256);
+    return at;
+  };
+  memset(l, 0, sizeof(*l));
+  l->row_capacity = rows;
+  l->num_chunks = chunks;
+  l->counts_offset = take(e_local * 4);
+  l->offsets_offset = take((e_local + 1) * 4);
+  l->meta_offset = take(16 * 4);
+  l->chunk_counts_offset = take((chunks > 0 ? chunks : 1) * e_local * 4);
+  l->output_index_offset = take((tasks > 0 ? tasks : 1) * 4);
+  l->row_token_offset = take(rows * 4);
+  l->row_weight_offset = take(rows * 4);
+  l->m_indices_offset = take(rows * 4);
+  l->act_scale_offset = take(rows * 4);
+  l->h_offset = take(rows * 2 * intermediate * 2);
+  l->act_offset = take(rows * static_cast<int64_t>(intermediate));
+  l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
+  l->total_bytes = off;
+}
+
+void plan_symm(int num_max_tokens, int num_topk, int hidden, mmoe_symm_layout* s) {
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t at = off;
+    off = align_up(off + bytes, 256);
+    return at;
+  };
+  memset(s, 0, sizeof(*s));
+  const int64_t t = num_max_tokens;
+  s->runtime_num_tokens_offset = take(16);
+  s->x_offset = take(t * hidden);
+  s->x_sf_offset = take(t * 4);
+  s->topk_idx_offset = take(t * num_topk * 8);
+  s->topk_weights_offset = take(t * num_topk * 4);
+  s->total_bytes = off;
+}
+
+std::atomic<int> g_cu_cache[64];
+
+int device_cus(int* out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MMOE_ERR_NO_DEVICE;
+  if (dev >= 0 && dev < 64) {
+    const int cached = g_cu_cache[dev].load(std::memory_order_relaxed);
+    if (cached > 0) {
+      *out = cached;
+      return MMOE_OK;
+    }
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return MMOE_ERR_NO_DEVICE;
+  if (dev >= 0 && dev < 64) g_cu_cache[dev].store(cus, std::memory_order_relaxed);
+  *out = cus;
+  return MMOE_OK;
+}
+
+template <class T>
+T* at(void* base, int64_t off) {
+  return reinterpret_cast<T*>(static_cast<uint8_t*>(base) + off);
+}
+
+int validate_forward(const mmoe_forward_args* a) {
+  if (a == nullptr) return MMOE_ERR_NULL_POINTER;
+  int st = check_common(1, a->num_experts, a->num_max_tokens, a->num_topk, a->hidden,
+                        a->intermediate);
+  if (st != MMOE_OK) return st;
+  if (a->hidden % 16 || a->intermediate % 16) return MMOE_ERR_MARLIN_DIVISIBLE;
+  if (a->num_tokens < 0) return MMOE_ERR_ARGUMENT;
+  if (a->num_tokens > a->num_max_tokens) return MMOE_ERR_TOO_MANY_TOKENS;
+  if (!mmoe::gemm_shape_supported(2 * a->intermediate, a->hidden) ||
+      !mmoe::gemm_shape_supported(a->hidden, a->intermediate))
+    return MMOE_ERR_UNSUPPORTED_SHAPE;
+  if (a->schedule < MMOE_SCHEDULE_AUTO || a->schedule > MMOE_SCHEDULE_STAGED)
+    return MMOE_ERR_SCHEDULE;
+  mmoe_symm_layout sl;
+  plan_symm(a->num_max_tokens, a->num_topk, a->hidden, &sl);
+  if (a->sym_buffer_bytes >= 0 && a->sym_buffer_bytes < sl.total_bytes)
+    return MMOE_ERR_SYM_BUFFER_SMALL;
+  mmoe_scratch_layout l;
+  plan_scratch(1, a->num_experts, a->num_max_tokens, a->num_topk, a->hidden, a->intermediate,
+               &l);
+  if (a->route_scratch_bytes < l.total_bytes) return MMOE_ERR_SCRATCH_SMALL;
+  if (a->num_tokens > 0 &&
+      (a->y == nullptr || a->x == nullptr || a->x_sf == nullptr || a->topk_idx == nullptr ||
+       a->topk_weights == nullptr || a->w1 == nullptr || a->w1_sf == nullptr ||
+       a->w2 == nullptr || a->w2_sf == nullptr || a->route_scratch == nullptr))
+    return MMOE_ERR_NULL_POINTER;
+  return MMOE_OK;
+}
+
+mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratch_layout& l) {
+  mmoe::RouteArgs r;
+  memset(&r, 0, sizeof(r));
+  void* ws = a->route_scratch;
+  r.topk_idx = a->topk_idx;
+  r.idx_i64 = 1;
+  r.topk_w = a->topk_weights;
+  r.runtime_tokens = a->runtime_num_tokens;
+  r.host_tokens = a->num_tokens;
+  r.topk = a->num_topk;
+  r.num_experts = a->num_experts;
+  r.check_weight = 1;
+  r.row_cap = l.row_capacity;
+  r.chunk_counts = at<int32_t>(ws, l.chunk_counts_offset);
+  r.counts = at<int32_t>(ws, l.counts_offset);
+  r.offsets = at<int32_t>(ws, l.offsets_offset);
+  r.meta = at<int32_t>(ws, l.meta_offset);
+  r.stats = a->stats;
+  r.given_counts = nullptr;
+  r.output_index = at<int32_t>(ws, l.output_index_offset);
+  r.row_token = at<int32_t>(ws, l.row_token_offset);
+  r.row_weight = at<float>(ws, l.row_weight_offset);
+  r.m_indices = at<int32_t>(ws, l.m_indices_offset);
+  return r;
+}
+
+int run_route(const mmoe_forward_args* a, const mmoe_scratch_layout& l, hipStream_t s) {
+  const mmoe::RouteArgs r = forward_route_args(a, l);
+  const int64_t tasks = static_cast<int64_t>(a->num_tokens) * a->num_topk;
+  const int64_t chunks = (tasks + mmoe::kRouteChunk - 1) / mmoe::kRouteChunk;
+  return mmoe::launch_route(r, chunks, s) == hipSuccess ? MMOE_OK : MMOE_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mmoe_token_alignment(void) { return kTokenAlignment; }
+
+int mmoe_symm_buffer_layout(int num_ranks, int num_experts, int num_max_tokens, int num_topk,
+                            int hidden, int intermediate, mmoe_symm_layout* out) {
+  if (out == nullptr) return MMOE_ERR_NULL_POINTER;
+  const int st = check_common(num_ranks, num_experts, num_max_tokens, num_topk, hidden,
+                              intermediate);
+  if (st != MMOE_OK) return st;
+  plan_symm(num_max_tokens, num_topk, hidden, out);
+  return MMOE_OK;
+}
+
+int mmoe_route_scratch_layout(int num_ranks, int num_experts, int num_max_tokens, int num_topk,
+                              int hidden, int intermediate, mmoe_scratch_layout* out) {
+  if (out == nullptr) return MMOE_ERR_NULL_POINTER;
+  const int st = check_common(num_ranks, num_experts, num_max_tokens, num_topk, hidden,
+                              intermediate);
+  if (st != MMOE_OK) return st;
+  plan_scratch(num_ranks, num_experts, num_max_tokens, num_topk, hidden, intermediate, out);
+  return MMOE_OK;
+}
+
+int mmoe_route_scratch_bytes(int num_ranks, int num_experts, int num_max_tokens, int num_topk,
+                             int hidden, int intermediate, int64_t* out_bytes) {
+  if (out_bytes == nullptr) return MMOE_ERR_NULL_POINTER;
+  mmoe_scratch_layout l;
+  const int st = mmoe_route_scratch_layout(num_ranks, num_experts, num_max_tokens, num_topk,
+                                           hidden, intermediate, &l);
+  if (st != MMOE_OK) return st;
+  *out_bytes = l.total_bytes;
+  return MMOE_OK;
+}
+
+const char* mmoe_build_config(void) {
+  return "{\"operator\": \"fp8_w8a8_mega_moe\", \"package\": \"megamoe\", "
+         "\"arch\": \"gfx950\", \"fp8_format\": \"e4m3fn (OCP)\", "
+         "\"weight_scale_mode\": \"channelwise_fp32\", \"input_scale_mode\": "
+         "\"channelwise_fp32\", \"l2_act_scale_mode\": \"channelwise_fp32\", "
+         "\"has_fp8_api\": true, \"has_fp4_api\": false, \"mfma\": "
+         "\"v_mfma_f32_32x32x64_f8f6f4\", \"fusion_boundary\": "
+         "\"route|gemm1(gather)|swiglu_quant|gemm2|combine\", \"num_ranks\": 1}";
+}
+
+const char* mmoe_status_string(int status) {
+  switch (status) {
+    case MMOE_OK: return "ok";
+    case MMOE_ERR_NULL_POINTER: return "a required pointer is null";
+    case MMOE_ERR_NUM_RANKS: return "num_ranks must be positive";
+    case MMOE_ERR_EXPERTS_DIVISIBLE: return "num_experts must be divisible by num_ranks";
+    case MMOE_ERR_HIDDEN_SIZES: return "hidden sizes must be positive";
+    case MMOE_ERR_MARLIN_DIVISIBLE:
+      return "DCU MegaMoE Marlin weights require rows and K divisible by 16";
+    case MMOE_ERR_TOO_MANY_TOKENS: return "too many tokens";
+    case MMOE_ERR_SYM_BUFFER_SMALL:
+      return "sym_buffer is too small for the requested DCU MegaMoE capacity";
+    case MMOE_ERR_SCRATCH_SMALL:
+      return "route_scratch is too small for the requested DCU MegaMoE capacity";
+    case MMOE_ERR_UNSUPPORTED_SHAPE:
+      return "unsupported shape: hidden and intermediate must be multiples of 128, "
+             "1 <= experts <= 1024";
+    case MMOE_ERR_TOPK: return "num_topk must be in 1..16";
+    case MMOE_ERR_SCHEDULE: return "unknown schedule override";
+    case MMOE_ERR_HIP: return "HIP kernel launch failed";
+    case MMOE_ERR_NO_DEVICE: return "no usable HIP device";
+    case MMOE_ERR_ARGUMENT: return "invalid argument";
+    default: return "unknown status";
+  }
+}
+
+int mmoe_route(const mmoe_forward_args* a, void* stream) {
+  const int st = validate_forward(a);
+  if (st != MMOE_OK) return st;
+  mmoe_scratch_layout l;
+  plan_scratch(1, a->num_experts, a->num_max_tokens, a->num_topk, a->hidden, a->intermediate,
+               &l);
+  if (a->num_tokens == 0) return MMOE_OK;
+  return run_route(a, l, static_cast<hipStream_t>(stream));
+}
+
+int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_stage,
+                        void* stream) {
+  int st = validate_forward(a);
+  if (st != MMOE_OK) return st;
+  if (first_stage < MMOE_STAGE_ROUTE || last_stage > MMOE_STAGE_COMBINE ||
+      first_stage > last_stage)
+    return MMOE_ERR_ARGUMENT;
+  if (a->num_tokens == 0) return MMOE_OK;
+  int cus = 0;
+  st = device_cus(&cus);
+  if (st != MMOE_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mmoe_scratch_layout l;
+  plan_scratch(1, a->num_experts, a->num_max_tokens, a->num_topk, a->hidden, a->intermediate,
+               &l);
+  auto runs = [&](int stage) { return first_stage <= stage && stage <= last_stage; };
+
+  const int threshold = a->token_threshold > 0 ? a->token_threshold : kDefaultThreshold;
+  bool staged = a->num_tokens > threshold;
+  if (a->schedule == MMOE_SCHEDULE_PERSISTENT) staged = false;
+  if (a->schedule == MMOE_SCHEDULE_STAGED) staged = true;
+  const mmoe::GemmShape shape = staged ? mmoe::GemmShape::kPrefill : mmoe::GemmShape::kDecode;
+  const int max_rows = a->num_tokens * a->num_topk;
+  void* ws = a->route_scratch;
+
+  if (runs(MMOE_STAGE_ROUTE)) {
+    st = run_route(a, l, s);
+    if (st != MMOE_OK) return st;
+  }
+
+  mmoe::GemmArgs g1;
+  g1.a = static_cast<const uint8_t*>(a->x);
+  g1.row_token = at<int32_t>(ws, l.row_token_offset);
+  g1.a_scale = a->x_sf;
+  g1.lda = a->hidden;
+  g1.b = static_cast<const uint8_t*>(a->w1);
+  g1.b_scale = a->w1_sf;
+  g1.c = at<uint16_t>(ws, l.h_offset);
+  g1.counts = at<int32_t>(ws, l.counts_offset);
+  g1.offsets = at<int32_t>(ws, l.offsets_offset);
+  g1.num_experts = a->num_experts;
+  g1.n = 2 * a->intermediate;
+  g1.k = a->hidden;
+  if (runs(MMOE_STAGE_GEMM1) &&
+      mmoe::launch_grouped_gemm(g1, shape, max_rows, cus, s) != hipSuccess)
+    return MMOE_ERR_HIP;
+
+  if (runs(MMOE_STAGE_SWIGLU)) {
+    mmoe::SwigluArgs sw;
+    sw.h = at<uint16_t>(ws, l.h_offset);
+    sw.row_weight = at<float>(ws, l.row_weight_offset);
+    sw.meta = at<int32_t>(ws, l.meta_offset);
+    sw.act = at<uint8_t>(ws, l.act_offset);
+    sw.act_scale = at<float>(ws, l.act_scale_offset);
+    sw.inter = a->intermediate;
+    sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
+    sw.clamp = a->activation_clamp;
+    if (mmoe::launch_swiglu_quant(sw, max_rows, cus, s) != hipSuccess) return MMOE_ERR_HIP;
+  }
+
+  if (runs(MMOE_STAGE_GEMM2)) {
+    mmoe::GemmArgs g2 = g1;
+    g2.a = at<uint8_t>(ws, l.act_offset);
+    g2.row_token = nullptr;
+    g2.a_scale = at<float>(ws, l.act_scale_offset);
+    g2.lda = a->intermediate;
+    g2.b = static_cast<const uint8_t*>(a->w2);
+    g2.b_scale = a->w2_sf;
+    g2.c = at<uint16_t>(ws, l.part_offset);
+    g2.n = a->hidden;
+    g2.k = a->intermediate;
+    if (mmoe::launch_grouped_gemm(g2, shape, max_rows, cus, s) != hipSuccess) return MMOE_ERR_HIP;
+  }
+
+  if (runs(MMOE_STAGE_COMBINE)) {
+    mmoe::CombineArgs c;
+    memset(&c, 0, sizeof(c));
+    c.y = static_cast<uint16_t*>(a->y);
+    c.part = at<uint16_t>(ws, l.part_offset);
+    c.output_index = at<int32_t>(ws, l.output_index_offset);
+    c.runtime_tokens = a->runtime_num_tokens;
+    c.host_tokens = a->num_tokens;
+    c.topk = a->num_topk;
+    c.hidden = a->hidden;
+    if (mmoe::launch_combine(c, cus, s) != hipSuccess) return MMOE_ERR_HIP;
+  }
+  return MMOE_OK;
+}
+
+int mmoe_forward(const mmoe_forward_args* a, void* stream) {
+  return mmoe_forward_stages(a, MMOE_STAGE_ROUTE, MMOE_STAGE_COMBINE, stream);
+}
+
+int mmoe_deepep_preprocess_workspace_bytes(int recv_rows, int topk, int num_experts,
+                                           int total_rows, int64_t* out_bytes) {
+  if (out_bytes == nullptr) return MMOE_ERR_NULL_POINTER;
+  if (recv_rows < 0 || topk <= 0 || num_experts <= 0 || num_experts > mmoe::kMaxExperts ||
+      total_rows < 0)
+    return MMOE_ERR_ARGUMENT;
+  const int64_t tasks = static_cast<int64_t>(recv_rows) * topk;
+  const int64_t chunks = (tasks + mmoe::kRouteChunk - 1) / mmoe::kRouteChunk;
+  int64_t off = 0;
+  off = align_up(off + num_experts * 4, 256);            // counts
+  off = align_up(off + (num_experts + 1) * 4, 256);      // offsets
+  off = align_up(off + 16 * 4, 256);                     // meta
+  off = align_up(off + (chunks > 0 ? chunks : 1) * num_experts * 4, 256);
+  off = align_up(off + (total_rows > 0 ? total_rows : 1) * 4, 256);  // row_token
+  *out_bytes = off;
+  return MMOE_OK;
+}
+
+int mmoe_deepep_preprocess_channelwise(void* grouped_x, float* grouped_x_scale,
+                                       float* route_weights, int32_t* m_indices,
+                                       int32_t* output_index, const void* recv_x,
+                                       const float* recv_x_scale, const void* recv_topk_ids,
+                                       const float* recv_topk_weights,
+                                       const int32_t* num_recv_tokens_per_expert,
+                                       int total_rows, int recv_rows, int topk, int hidden,
+                                       int num_experts, int topk_ids_i64, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  int64_t need = 0;
+  int st = mmoe_deepep_preprocess_workspace_bytes(recv_rows, topk, num_experts, total_rows, &need);
+  if (st != MMOE_OK) return st;
+  if (workspace_bytes < need) return MMOE_ERR_SCRATCH_SMALL;
+  if (hidden <= 0) return MMOE_ERR_HIDDEN_SIZES;
+  const int64_t tasks = static_cast<int64_t>(recv_rows) * topk;
+  if (tasks == 0) return MMOE_OK;
+  if (grouped_x == nullptr || grouped_x_scale == nullptr || route_weights == nullptr ||
+      m_indices == nullptr || output_index == nullptr || recv_x == nullptr ||
+      recv_x_scale == nullptr || recv_topk_ids == nullptr || recv_topk_weights == nullptr ||
+      num_recv_tokens_per_expert == nullptr || workspace == nullptr)
+    return MMOE_ERR_NULL_POINTER;
+  const int64_t chunks = (tasks + mmoe::kRouteChunk - 1) / mmoe::kRouteChunk;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t a0 = off;
+    off = align_up(off + bytes, 256);
+    return a0;
+  };
+  mmoe::RouteArgs r;
+  memset(&r, 0, sizeof(r));
+  r.counts = at<int32_t>(workspace, take(num_experts * 4));
+  r.offsets = at<int32_t>(workspace, take((num_experts + 1) * 4));
+  r.meta = at<int32_t>(workspace, take(16 * 4));
+  r.chunk_counts = at<int32_t>(workspace, take(chunks * num_experts * 4));
+  r.row_token = at<int32_t>(workspace, take((total_rows > 0 ? total_rows : 1) * 4));
+  r.topk_idx = recv_topk_ids;
+  r.idx_i64 = topk_ids_i64 ? 1 : 0;
+  r.topk_w = recv_topk_weights;
+  r.host_tokens = recv_rows;
+  r.topk = topk;
+  r.num_experts = num_experts;
+  r.check_weight = 0;
+  r.row_cap = total_rows;
+  r.given_counts = num_recv_tokens_per_expert;
+  r.output_index = output_index;
+  r.row_weight = route_weights;
+  r.m_indices = m_indices;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mmoe::launch_route(r, chunks, s) != hipSuccess) return MMOE_ERR_HIP;
+  if (mmoe::launch_gather_tasks(static_cast<uint8_t*>(grouped_x), grouped_x_scale,
+                                static_cast<const uint8_t*>(recv_x), recv_x_scale, output_index,
+                                tasks, topk, hidden, s) != hipSuccess)
+    return MMOE_ERR_HIP;
+  return MMOE_OK;
+}
+
+int mmoe_deepep_postprocess_channelwise(void* recv_y, const void* l2_out,
+                                        const void* recv_topk_ids,
+                                        const float* recv_topk_weights,
+                                        const int32_t* output_index, int recv_rows, int topk,
+                                        int hidden, int topk_ids_i64, int apply_topk_weights,
+                                        void* stream) {
+  if (recv_rows < 0 || topk <= 0 || topk > kMaxTopk || hidden <= 0) return MMOE_ERR_ARGUMENT;
+  if (recv_rows == 0) return MMOE_OK;
+  if (recv_y == nullptr || l2_out == nullptr || recv_topk_ids == nullptr ||
+      recv_topk_weights == nullptr || output_index == nullptr)
+    return MMOE_ERR_NULL_POINTER;
+  int cus = 0;
+  const int st = device_cus(&cus);
+  if (st != MMOE_OK) return st;
+  mmoe::CombineArgs c;
+  memset(&c, 0, sizeof(c));
+  c.y = static_cast<uint16_t*>(recv_y);
+  c.part = static_cast<const uint16_t*>(l2_out);
+  c.output_index = output_index;
+  c.topk_ids = recv_topk_ids;
+  c.ids_i64 = topk_ids_i64 ? 1 : 0;
+  c.topk_w = recv_topk_weights;
+  c.apply_weights = apply_topk_weights ? 1 : 0;
+  c.host_tokens = recv_rows;
+  c.topk = topk;
+  c.hidden = hidden;
+  return mmoe::launch_combine(c, cus, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? MMOE_OK
+             : MMOE_ERR_HIP;
+}
+
+int mmoe_cast_fp8_channelwise(void* out_fp8, float* out_scale, const void* x_bf16, int64_t rows,
+                              int64_t cols, void* stream) {
+  if (rows < 0 || cols <= 0) return MMOE_ERR_ARGUMENT;
+  if (rows == 0) return MMOE_OK;
+  if (out_fp8 == nullptr || out_scale == nullptr || x_bf16 == nullptr) return MMOE_ERR_NULL_POINTER;
+  return mmoe::launch_cast_fp8_channelwise(static_cast<uint8_t*>(out_fp8), out_scale,
+                                           static_cast<const uint16_t*>(x_bf16), rows, cols,
+                                           static_cast<hipStream_t>(stream)) == hipSuccess
+             ? MMOE_OK
+             : MMOE_ERR_HIP;
+}
+
+int mmoe_marlin_pack(void* out, const void* in, int64_t groups, int64_t rows, int64_t k,
+                     void* stream) {
+  if (groups < 0 || rows < 0 || k < 0) return MMOE_ERR_ARGUMENT;
+  if (rows % 16 || k % 16) return MMOE_ERR_MARLIN_DIVISIBLE;
+  if (groups * rows * k == 0) return MMOE_OK;
+  if (out == nullptr || in == nullptr) return MMOE_ERR_NULL_POINTER;
+  return mmoe::launch_marlin_pack(static_cast<uint8_t*>(out), static_cast<const uint8_t*>(in),
+                                  groups, rows, k, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? MMOE_OK
+             : MMOE_ERR_HIP;
+}
+
+int mmoe_debug_f32_to_e4m3(uint8_t* out, const float* in, int64_t n, void* stream) {
+  if (n < 0) return MMOE_ERR_ARGUMENT;
+  if (n == 0) return MMOE_OK;
+  if (out == nullptr || in == nullptr) return MMOE_ERR_NULL_POINTER;
+  return mmoe::launch_f32_to_e4m3(out, in, n, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? MMOE_OK
+             : MMOE_ERR_HIP;
+}
+
+}  // extern "C"

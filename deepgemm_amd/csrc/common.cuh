@@ -1,0 +1,75 @@
+// common.cuh -- gfx950 device helpers shared by the Mega MoE kernels.
+//
+// Number formats: OCP FP8 E4M3 (e4m3fn, the bytes of torch.float8_e4m3fn) for activations
+// and weights; bf16 with round-to-nearest-even for the GEMM outputs and the layer output.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mmoe {
+
+constexpr float kE4m3Max = 448.0f;
+constexpr float kAmaxFloor = 1.0e-4f;
+constexpr int kWave = 64;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (finite inputs; the layer never produces NaN/Inf from
+// finite FP8 operands and finite scales).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+__device__ __forceinline__ float clip_e4m3(float v) {
+  return fminf(kE4m3Max, fmaxf(-kE4m3Max, v));
+}
+
+// Four floats -> four e4m3fn bytes (little-endian in one u32). Clip to +-448 first, then the
+// gfx950 hardware conversion (round to nearest even, OCP encoding).
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+  int p = __builtin_amdgcn_cvt_pk_fp8_f32(clip_e4m3(a), clip_e4m3(b), 0, false);
+  p = __builtin_amdgcn_cvt_pk_fp8_f32(clip_e4m3(c), clip_e4m3(d), p, true);
+  return static_cast<uint32_t>(p);
+}
+
+__device__ __forceinline__ uint8_t f32_to_e4m3(float a) {
+  int p = __builtin_amdgcn_cvt_pk_fp8_f32(clip_e4m3(a), 0.0f, 0, false);
+  return static_cast<uint8_t>(p & 0xff);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
+
+// Number of tokens this call processes: the device scalar (clamped to [0, cap]) when given,
+// else the host value.
+__device__ __forceinline__ int effective_tokens(const int32_t* runtime_tokens, int host_tokens) {
+  if (runtime_tokens == nullptr) return host_tokens;
+  int v = *runtime_tokens;
+  return v < 0 ? 0 : (v > host_tokens ? host_tokens : v);
+}
+
+}  // namespace mmoe

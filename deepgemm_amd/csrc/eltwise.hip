@@ -1,0 +1,300 @@
+// eltwise.hip -- the HBM-bound stages around the GEMMs (gfx950):
+//   * SwiGLU x route weight + per-row e4m3 requant (the reference's K2,
+//     megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:254-377), one wave per row;
+//   * the top-k combine as an inverse-index gather (no atomics, fixed slot order):
+//     y[t] = bf16(sum_s f32(part[output_index[t,s]])), the reference's reduce
+//     (deep_gemm/include/deep_gemm/impls/mega_moe_dcu.cuh:706-760) and baseline gather
+//     (csrc/kernels/mega_moe_baseline_hip.cu:98-127);
+//   * row gather for the DeepEP-style preprocess, channelwise FP8 cast, Marlin pack.
+#include "common.cuh"
+#include "kernels.h"
+
+namespace mmoe {
+
+namespace {
+
+constexpr int kEltThreads = 256;
+constexpr int kEltWaves = kEltThreads / kWave;
+
+// ---------------------------------------------------------------- SwiGLU + requant
+// Lane j of the wave owns 4-element groups j, j+64, ...; kGroups = ceil(I/4/64) per lane.
+template <int kGroups>
+__global__ __launch_bounds__(kEltThreads) void swiglu_quant_kernel(SwigluArgs s) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int rows = s.meta[0];
+  const int inter = s.inter;
+  const int ngroups = inter >> 2;
+  for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
+    const float w = s.row_weight[row];
+    uint8_t* out = s.act + static_cast<int64_t>(row) * inter;
+    if (w == 0.0f) {
+      for (int gi = lane; gi < ngroups; gi += kWave) reinterpret_cast<uint32_t*>(out)[gi] = 0u;
+      if (lane == 0) s.act_scale[row] = kAmaxFloor / kE4m3Max;
+      continue;
+    }
+    const uint16_t* hrow = s.h + static_cast<int64_t>(row) * 2 * inter;
+    float y[kGroups][4];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kGroups; ++j) {
+      const int gi = lane + j * kWave;
+      if (gi < ngroups) {
+        const uint2 gv = *reinterpret_cast<const uint2*>(hrow + gi * 4);
+        const uint2 uv = *reinterpret_cast<const uint2*>(hrow + inter + gi * 4);
+        float gate[4] = {bf16_to_f32(gv.x & 0xffff), bf16_to_f32(gv.x >> 16),
+                         bf16_to_f32(gv.y & 0xffff), bf16_to_f32(gv.y >> 16)};
+        float up[4] = {bf16_to_f32(uv.x & 0xffff), bf16_to_f32(uv.x >> 16),
+                       bf16_to_f32(uv.y & 0xffff), bf16_to_f32(uv.y >> 16)};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float gq = gate[q], uq = up[q];
+          if (s.has_clamp) {
+            uq = fminf(s.clamp, fmaxf(-s.clamp, uq));
+            gq = fminf(s.clamp, gq);
+          }
+          const float v = gq * (1.0f / (1.0f + expf(-gq))) * uq * w;
+          y[j][q] = v;
+          amax = fmaxf(amax, fabsf(v));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) y[j][q] = 0.0f;
+      }
+    }
+    amax = wave_max(amax);
+    const float a = fmaxf(amax, kAmaxFloor);
+    const float inv = kE4m3Max / a;
+    if (lane == 0) s.act_scale[row] = a / kE4m3Max;
+#pragma unroll
+    for (int j = 0; j < kGroups; ++j) {
+      const int gi = lane + j * kWave;
+      if (gi < ngroups)
+        reinterpret_cast<uint32_t*>(out)[gi] =
+            pack_e4m3x4(y[j][0] * inv, y[j][1] * inv, y[j][2] * inv, y[j][3] * inv);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- combine
+// One workgroup per token (grid-stride); each thread owns 8-element (16-byte) columns.
+__global__ __launch_bounds__(kEltThreads) void combine_kernel(CombineArgs c) {
+  __shared__ int s_rows[16];
+  __shared__ float s_w[16];
+  const int tokens = effective_tokens(c.runtime_tokens, c.host_tokens);
+  const int nvec = c.hidden >> 3;
+  for (int t = blockIdx.x; t < tokens; t += gridDim.x) {
+    if (threadIdx.x < c.topk) {
+      const int64_t route = static_cast<int64_t>(t) * c.topk + threadIdx.x;
+      int row = c.output_index[route];
+      float w = 1.0f;
+      if (c.topk_ids != nullptr) {
+        const int64_t ex = c.ids_i64 ? static_cast<const int64_t*>(c.topk_ids)[route]
+                                     : static_cast<const int32_t*>(c.topk_ids)[route];
+        if (ex < 0) row = -1;
+      }
+      if (c.apply_weights) w = c.topk_w[route];
+      s_rows[threadIdx.x] = row;
+      s_w[threadIdx.x] = w;
+    }
+    __syncthreads();
+    uint4* yrow = reinterpret_cast<uint4*>(c.y + static_cast<int64_t>(t) * c.hidden);
+    for (int v = threadIdx.x; v < nvec; v += kEltThreads) {
+      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < c.topk; ++s) {
+        const int row = s_rows[s];
+        if (row < 0) continue;
+        const uint4 p = reinterpret_cast<const uint4*>(c.part + static_cast<int64_t>(row) * c.hidden)[v];
+        const uint32_t words[4] = {p.x, p.y, p.z, p.w};
+        const float w = s_w[s];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float lo = bf16_to_f32(words[q] & 0xffff);
+          float hi = bf16_to_f32(words[q] >> 16);
+          if (c.apply_weights) { lo *= w; hi *= w; }
+          sum[2 * q] += lo;
+          sum[2 * q + 1] += hi;
+        }
+      }
+      uint4 o;
+      o.x = pack_bf16x2(sum[0], sum[1]);
+      o.y = pack_bf16x2(sum[2], sum[3]);
+      o.z = pack_bf16x2(sum[4], sum[5]);
+      o.w = pack_bf16x2(sum[6], sum[7]);
+      yrow[v] = o;
+    }
+    __syncthreads();
+  }
+}
+
+// Scalar tail of the combine for hidden % 8 != 0 (kept simple; the layer uses H % 128 == 0).
+__global__ __launch_bounds__(kEltThreads) void combine_scalar_kernel(CombineArgs c) {
+  const int tokens = effective_tokens(c.runtime_tokens, c.host_tokens);
+  for (int t = blockIdx.x; t < tokens; t += gridDim.x) {
+    for (int h = threadIdx.x; h < c.hidden; h += kEltThreads) {
+      float sum = 0.0f;
+      for (int s = 0; s < c.topk; ++s) {
+        const int64_t route = static_cast<int64_t>(t) * c.topk + s;
+        const int row = c.output_index[route];
+        if (row < 0) continue;
+        if (c.topk_ids != nullptr) {
+          const int64_t ex = c.ids_i64 ? static_cast<const int64_t*>(c.topk_ids)[route]
+                                       : static_cast<const int32_t*>(c.topk_ids)[route];
+          if (ex < 0) continue;
+        }
+        float v = bf16_to_f32(c.part[static_cast<int64_t>(row) * c.hidden + h]);
+        if (c.apply_weights) v *= c.topk_w[route];
+        sum += v;
+      }
+      c.y[static_cast<int64_t>(t) * c.hidden + h] = f32_to_bf16(sum);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- task gather (preprocess)
+__global__ __launch_bounds__(kEltThreads) void gather_tasks_kernel(uint8_t* gx, float* gs,
+                                                                   const uint8_t* x,
+                                                                   const float* x_sf,
+                                                                   const int32_t* output_index,
+                                                                   int64_t tasks, int topk,
+                                                                   int hidden) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  for (int64_t task = static_cast<int64_t>(blockIdx.x) * kEltWaves + wave; task < tasks;
+       task += static_cast<int64_t>(gridDim.x) * kEltWaves) {
+    const int64_t r = output_index[task];
+    if (r < 0) continue;
+    const int64_t tok = task / topk;
+    const uint8_t* src = x + static_cast<int64_t>(tok) * hidden;
+    uint8_t* dst = gx + r * hidden;
+    if ((hidden & 15) == 0) {
+      for (int v = lane; v < (hidden >> 4); v += kWave)
+        reinterpret_cast<uint4*>(dst)[v] = reinterpret_cast<const uint4*>(src)[v];
+    } else {
+      for (int v = lane; v < hidden; v += kWave) dst[v] = src[v];
+    }
+    if (lane == 0) gs[r] = x_sf[tok];
+  }
+}
+
+// ---------------------------------------------------------------- channelwise cast
+__global__ __launch_bounds__(kEltThreads) void cast_fp8_rows_kernel(uint8_t* out, float* scale,
+                                                                    const uint16_t* x,
+                                                                    int64_t rows, int64_t cols) {
+  __shared__ float s_red[kEltWaves];
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const uint16_t* xr = x + r * cols;
+    float amax = 0.0f;
+    for (int64_t c = threadIdx.x; c < cols; c += kEltThreads) amax = fmaxf(amax, fabsf(bf16_to_f32(xr[c])));
+    amax = wave_max(amax);
+    if (lane_id() == 0) s_red[threadIdx.x / kWave] = amax;
+    __syncthreads();
+    float m = s_red[0];
+    for (int w = 1; w < kEltWaves; ++w) m = fmaxf(m, s_red[w]);
+    const float sc = fmaxf(m, kAmaxFloor) / kE4m3Max;
+    if (threadIdx.x == 0) scale[r] = sc;
+    uint8_t* orow = out + r * cols;
+    for (int64_t c = threadIdx.x; c < cols; c += kEltThreads) orow[c] = f32_to_e4m3(bf16_to_f32(xr[c]) / sc);
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- Marlin pack
+// out[g, r/16, (k/16)*256 + (r%16)*16 + k%16] = in[g, r, k]; one thread per 16-byte block row.
+__global__ __launch_bounds__(kEltThreads) void marlin_pack_kernel(uint8_t* out, const uint8_t* in,
+                                                                  int64_t groups, int64_t rows,
+                                                                  int64_t k) {
+  const int64_t kblocks = k >> 4;
+  const int64_t total = groups * rows * kblocks;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEltThreads + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * kEltThreads) {
+    const int64_t kb = i % kblocks;
+    const int64_t gr = i / kblocks;  // g * rows + r
+    const int64_t r = gr % rows;
+    const int64_t gidx = gr / rows;
+    const uint4 v = *reinterpret_cast<const uint4*>(in + gr * k + kb * 16);
+    const int64_t dst = ((gidx * (rows >> 4) + (r >> 4)) * k + kb * 16) * 16 + (r & 15) * 16;
+    *reinterpret_cast<uint4*>(out + dst) = v;
+  }
+}
+
+__global__ __launch_bounds__(kEltThreads) void f32_to_e4m3_kernel(uint8_t* out, const float* in,
+                                                                  int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEltThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kEltThreads)
+    out[i] = f32_to_e4m3(in[i]);
+}
+
+unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
+  int64_t g = (work_items + per_block - 1) / per_block;
+  if (g > cap) g = cap;
+  if (g < 1) g = 1;
+  return static_cast<unsigned>(g);
+}
+
+}  // namespace
+
+hipError_t launch_swiglu_quant(const SwigluArgs& s, int64_t max_rows, int num_cus,
+                               hipStream_t stream) {
+  if (max_rows <= 0) return hipSuccess;
+  const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 8);
+  const int groups = (s.inter / 4 + kWave - 1) / kWave;
+  if (groups <= 2) {
+    hipLaunchKernelGGL(swiglu_quant_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, s);
+  } else if (groups <= 8) {
+    hipLaunchKernelGGL(swiglu_quant_kernel<8>, dim3(grid), dim3(kEltThreads), 0, stream, s);
+  } else if (groups <= 16) {
+    hipLaunchKernelGGL(swiglu_quant_kernel<16>, dim3(grid), dim3(kEltThreads), 0, stream, s);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream) {
+  if (c.host_tokens <= 0) return hipSuccess;
+  if (c.topk > 16) return hipErrorInvalidValue;
+  const unsigned grid = grid_for(c.host_tokens, 1, static_cast<int64_t>(num_cus) * 16);
+  if ((c.hidden & 7) == 0) {
+    hipLaunchKernelGGL(combine_kernel, dim3(grid), dim3(kEltThreads), 0, stream, c);
+  } else {
+    hipLaunchKernelGGL(combine_scalar_kernel, dim3(grid), dim3(kEltThreads), 0, stream, c);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_tasks(uint8_t* grouped_x, float* grouped_scale, const uint8_t* x,
+                               const float* x_sf, const int32_t* output_index, int64_t tasks,
+                               int topk, int hidden, hipStream_t stream) {
+  if (tasks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_tasks_kernel, dim3(grid_for(tasks, kEltWaves, 8192)),
+                     dim3(kEltThreads), 0, stream, grouped_x, grouped_scale, x, x_sf,
+                     output_index, tasks, topk, hidden);
+  return hipGetLastError();
+}
+
+hipError_t launch_cast_fp8_channelwise(uint8_t* out, float* scale, const uint16_t* x,
+                                       int64_t rows, int64_t cols, hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(cast_fp8_rows_kernel, dim3(grid_for(rows, 1, 65536)), dim3(kEltThreads), 0,
+                     stream, out, scale, x, rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t launch_marlin_pack(uint8_t* out, const uint8_t* in, int64_t groups, int64_t rows,
+                              int64_t k, hipStream_t stream) {
+  const int64_t total = groups * rows * (k >> 4);
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(marlin_pack_kernel, dim3(grid_for(total, kEltThreads, 65536)),
+                     dim3(kEltThreads), 0, stream, out, in, groups, rows, k);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_to_e4m3(uint8_t* out, const float* in, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(f32_to_e4m3_kernel, dim3(grid_for(n, kEltThreads, 65536)), dim3(kEltThreads),
+                     0, stream, out, in, n);
+  return hipGetLastError();
+}
+
+}  // namespace mmoe

@@ -1,0 +1,101 @@
+// kernels.h -- host-side launch interfaces of the gfx950 kernels (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mmoe {
+
+constexpr int kRouteChunk = 1024;  // tasks per routing chunk (== MMOE_ROUTE_CHUNK)
+constexpr int kMaxExperts = 1024;  // LDS-resident per-expert tables in the routing kernels
+
+struct RouteArgs {
+  const void* topk_idx;           // int64 or int32 [S, K]
+  int idx_i64;
+  const float* topk_w;            // f32 [S, K]
+  const int32_t* runtime_tokens;  // device scalar or null
+  int host_tokens;                // S (upper bound when runtime_tokens is set)
+  int topk;
+  int num_experts;
+  int check_weight;               // forward rule: w != 0 required
+  int64_t row_cap;                // rows >= row_cap are dropped (output_index = -1)
+  int32_t* chunk_counts;          // [nchunks, E] (becomes per-chunk bases after the scan)
+  int32_t* counts;                // [E]
+  int32_t* offsets;               // [E+1]
+  int32_t* meta;                  // [16]; meta[0] = R
+  int32_t* stats;                 // [E] or null (+= counts)
+  const int32_t* given_counts;    // preprocess: offsets from caller counts, else null
+  int32_t* output_index;          // [S, K]
+  int32_t* row_token;             // [rows]
+  float* row_weight;              // [rows] or null
+  int32_t* m_indices;             // [rows] or null
+};
+
+// Count -> scan -> stable scatter. Deterministic: rows of an expert in ascending task order.
+hipError_t launch_route(const RouteArgs& a, int64_t num_chunks, hipStream_t stream);
+
+struct GemmArgs {
+  const uint8_t* a;          // e4m3 rows, row-major, lda bytes apart
+  const int32_t* row_token;  // non-null: A row r is a[row_token[r]] (gather), scale a_scale[token]
+  const float* a_scale;      // per token (gather) or per row
+  int64_t lda;
+  const uint8_t* b;          // e4m3 Marlin [E, N/16, K*16]
+  const float* b_scale;      // f32 [E, N]
+  uint16_t* c;               // bf16 [rows, N]
+  const int32_t* counts;     // [E]
+  const int32_t* offsets;    // [E+1]
+  int num_experts;
+  int n;
+  int k;
+};
+
+enum class GemmShape { kDecode, kPrefill };
+
+// Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
+// a_scale[r] * b_scale[e,n]). Persistent: the grid strides over (m-tile, n-tile) pairs
+// computed on device from counts.
+hipError_t launch_grouped_gemm(const GemmArgs& g, GemmShape shape, int max_rows, int num_cus,
+                               hipStream_t stream);
+bool gemm_shape_supported(int n, int k);
+
+struct SwigluArgs {
+  const uint16_t* h;          // bf16 [rows, 2I]
+  const float* row_weight;    // [rows]
+  const int32_t* meta;        // meta[0] = rows
+  uint8_t* act;               // e4m3 [rows, I]
+  float* act_scale;           // [rows]
+  int inter;
+  int has_clamp;
+  float clamp;
+};
+hipError_t launch_swiglu_quant(const SwigluArgs& s, int64_t max_rows, int num_cus,
+                               hipStream_t stream);
+
+struct CombineArgs {
+  uint16_t* y;                     // bf16 [S, H]
+  const uint16_t* part;            // bf16 [rows, H]
+  const int32_t* output_index;     // [S, K]
+  const void* topk_ids;            // optional validity/weight source (postprocess)
+  int ids_i64;
+  const float* topk_w;             // applied when apply_weights
+  int apply_weights;
+  const int32_t* runtime_tokens;
+  int host_tokens;
+  int topk;
+  int hidden;
+};
+hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream);
+
+// For every task (token t, slot s) with row = output_index[t*K+s] >= 0:
+// grouped_x[row] = x[t], grouped_scale[row] = x_sf[t].
+hipError_t launch_gather_tasks(uint8_t* grouped_x, float* grouped_scale, const uint8_t* x,
+                               const float* x_sf, const int32_t* output_index, int64_t tasks,
+                               int topk, int hidden, hipStream_t stream);
+
+hipError_t launch_cast_fp8_channelwise(uint8_t* out, float* scale, const uint16_t* x,
+                                       int64_t rows, int64_t cols, hipStream_t stream);
+hipError_t launch_marlin_pack(uint8_t* out, const uint8_t* in, int64_t groups, int64_t rows,
+                              int64_t k, hipStream_t stream);
+hipError_t launch_f32_to_e4m3(uint8_t* out, const float* in, int64_t n, hipStream_t stream);
+
+}  // namespace mmoe

@@ -1,0 +1,275 @@
+"""GPU parity of the gfx950 HIP path against the CPU oracle (through the C ABI).
+
+Bars: routing (counts, offsets, output_index, row tables, stats) bit-exact; conversions and
+layout kernels bit-exact; layer output calc_diff <= 1e-3 (north star), checked per stage."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import c_oracle
+from oracle import megamoe_oracle as O
+from tests._helpers import (cpu_weights, log, make_tokens, make_weights_gpu, run_layer,
+                            zipf_routing)
+
+pytestmark = pytest.mark.gpu
+
+CALC_DIFF_BAR = 1e-3  # north star: calc_diff(y, oracle) <= 1e-3
+
+
+@pytest.fixture(scope="module")
+def mm(cuda):
+    from deepgemm_amd import megamoe
+    return megamoe
+
+
+# ------------------------------------------------------------------ conversions / layout
+def test_e4m3_conversion_matches_c_oracle(mm, cuda):
+    from tests.test_oracle import _probe_floats
+    f = _probe_floats()
+    out = torch.empty(f.size, dtype=torch.uint8, device=cuda)
+    inp = torch.from_numpy(f).to(cuda)
+    log(f"e4m3 conversion: {f.size} probes")
+    mm._capi.check(mm._capi.load().mmoe_debug_f32_to_e4m3(out.data_ptr(), inp.data_ptr(), f.size,
+                                                          mm._stream_handle()))
+    ref = np.empty(f.size, dtype=np.uint8)
+    c_oracle().oracle_e4m3_from_f32_array(ref.ctypes.data, f.ctypes.data, f.size)
+    got = out.cpu().numpy()
+    bad = np.nonzero(got != ref)[0]
+    assert bad.size == 0, f"{f[bad[:8]]} gpu={got[bad[:8]]} ref={ref[bad[:8]]}"
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 16), (37, 4096), (300, 2048), (5, 130)])
+def test_cast_fp8_channelwise_bitwise(mm, cuda, rows, cols):
+    gen = torch.Generator().manual_seed(rows * 7 + cols)
+    x = (torch.randn((rows, cols), generator=gen) * 3).to(torch.bfloat16)
+    x[0, :] = 0.0  # an all-zero row: scale 1e-4/448
+    log(f"cast rows={rows} cols={cols}")
+    q, s = mm.cast_to_fp8_channelwise(x.to(cuda))
+    qr, sr = O.cast_to_fp8_channelwise(x)
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu().view(torch.uint8), qr.view(torch.uint8))
+
+
+def test_marlin_pack_bitwise(mm, cuda):
+    w = torch.randint(0, 256, (3, 64, 256), dtype=torch.uint8).view(torch.float8_e4m3fn)
+    log("marlin pack")
+    got = mm.weight8bit_nt_kpack2_marlin(w.to(cuda)).cpu()
+    assert torch.equal(got.view(torch.uint8), O.marlin_pack(w).view(torch.uint8))
+
+
+# ------------------------------------------------------------------ routing
+ROUTE_CASES = {
+    # name: (S, E, K, global experts or "zipf"/"invalid")
+    "tiny": (5, 4, 3, None),
+    "c0": (64, 32, 6, None),
+    "c1": (1024, 32, 6, 256),
+    "ragged": (777, 32, 6, 256),
+    "zipf": (3000, 32, 6, "zipf"),
+    "wide": (2500, 40, 8, 64),
+}
+
+
+def _route_inputs(name):
+    s, e, k, g = ROUTE_CASES[name]
+    gen = torch.Generator().manual_seed(100 + s)
+    if g == "zipf":
+        idx, w = zipf_routing(s, e, k, gen)
+    else:
+        idx, w = O.make_routing(s, e, k, gen, g)
+    # sprinkle invalid cases: zero weights, ids out of range on both sides
+    if s > 4:
+        w[1, 0] = 0.0
+        idx[2, 1] = e
+        idx[3, 0] = -7
+    return idx, w, e, k
+
+
+@pytest.mark.parametrize("name", list(ROUTE_CASES))
+def test_routing_bit_exact(mm, cuda, name):
+    idx, w, e, k = _route_inputs(name)
+    s = idx.shape[0]
+    hidden, inter = 256, 128
+    log(f"routing case={name} S={s} E={e} K={k}")
+    buf = mm.SymmBuffer(None, e, s, k, hidden, inter)
+    buf.topk_idx[:s].copy_(idx)
+    buf.topk_weights[:s].copy_(w)
+    l1 = (torch.zeros((e, 2 * inter // 16, hidden * 16), dtype=torch.float8_e4m3fn, device=cuda),
+          torch.ones((e, 2 * inter), device=cuda))
+    l2 = (torch.zeros((e, hidden // 16, inter * 16), dtype=torch.float8_e4m3fn, device=cuda),
+          torch.ones((e, hidden), device=cuda))
+    stats0 = torch.randint(0, 100, (e,), dtype=torch.int32)
+    stats = stats0.to(cuda)
+    mm.route_only(s, l1, l2, buf, stats)
+    torch.cuda.synchronize()
+    ref = O.route(idx, w, e)
+    r = ref.num_rows
+    assert np.array_equal(buf.scratch_view("counts").cpu().numpy(), ref.counts)
+    assert np.array_equal(buf.scratch_view("offsets").cpu().numpy(), ref.offsets)
+    assert buf.scratch_view("meta")[0].item() == r
+    assert np.array_equal(buf.scratch_view("output_index")[:s].cpu().numpy(), ref.output_index)
+    assert np.array_equal(buf.scratch_view("row_token")[:r].cpu().numpy(), ref.row_token)
+    assert np.array_equal(buf.scratch_view("m_indices")[:r].cpu().numpy(), ref.m_indices)
+    assert np.array_equal(buf.scratch_view("row_weight")[:r].cpu().numpy(), ref.row_weight)
+    assert torch.equal(stats.cpu(), stats0 + torch.from_numpy(ref.counts))
+
+
+# ------------------------------------------------------------------ the layer
+def _stage_checks(buf, tr, s):
+    r = tr.routing.num_rows
+    h = buf.scratch_view("h")[:r].cpu()
+    assert O.calc_diff(h, tr.h) < 1e-5, "GEMM1 (gate||up) output"
+    act_s = buf.scratch_view("act_scale")[:r].cpu()
+    assert torch.allclose(act_s, tr.act_scale, rtol=2e-2, atol=0)
+    act = buf.scratch_view("act")[:r].cpu()
+    deq = act.float() * act_s.view(-1, 1)
+    deq_ref = tr.act.float() * tr.act_scale.view(-1, 1)
+    assert O.calc_diff(deq, deq_ref) < 1e-4, "SwiGLU requant"
+    part = buf.scratch_view("part")[:r].cpu()
+    assert O.calc_diff(part, tr.part) < 1e-3, "GEMM2 partials"
+
+
+@pytest.mark.parametrize("cfg", [
+    # (S, E, H, I, K, global experts, clamp)
+    (16, 4, 256, 128, 3, None, None),
+    (33, 8, 512, 256, 6, 16, None),
+    (64, 8, 512, 384, 4, None, 10.0),
+])
+def test_layer_small_shapes(mm, cuda, cfg):
+    s, e, hdim, inter, k, g, clamp = cfg
+    log(f"layer small cfg={cfg}")
+    x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=s + e, global_experts=g)
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=s * 3 + e, mm=mm)
+    buf = mm.SymmBuffer(None, e, s, k, hdim, inter)
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2, clamp=clamp)
+    torch.cuda.synchronize()
+    l1c, l2c = cpu_weights(l1, l2)
+    tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, activation_clamp=clamp)
+    _stage_checks(buf, tr, s)
+    d = O.calc_diff(y.cpu(), tr.y)
+    log(f"  calc_diff={d:.3e}")
+    assert d <= CALC_DIFF_BAR
+
+
+@pytest.fixture(scope="module")
+def full_weights(mm):
+    """Full-shape weights (32 experts, H=4096, I=2048), drawn on the GPU, plus CPU copies."""
+    log("full weights: drawing on GPU")
+    l1, l2 = make_weights_gpu(32, 4096, 2048, seed=1234, mm=mm)
+    torch.cuda.synchronize()
+    l1c, l2c = cpu_weights(l1, l2)
+    unpacked = (O.marlin_unpack(l1c[0], 4096, 4096), O.marlin_unpack(l2c[0], 4096, 2048))
+    return l1, l2, l1c, l2c, unpacked
+
+
+@pytest.mark.parametrize("case", ["c0", "c1_128", "ragged_77", "clamp10"])
+def test_layer_full_shape(mm, cuda, full_weights, case):
+    l1, l2, l1c, l2c, unpacked = full_weights
+    if case == "c0":
+        s, g, clamp = 64, None, None
+    elif case == "c1_128":
+        s, g, clamp = 1024, 256, None
+    elif case == "ragged_77":
+        s, g, clamp = 77, 64, None
+    else:
+        s, g, clamp = 96, None, 10.0
+    log(f"layer full-shape case={case} S={s}")
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, global_experts=g)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
+    stats = torch.zeros(32, dtype=torch.int32, device=cuda)
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2, clamp=clamp, stats=stats)
+    torch.cuda.synchronize()
+    tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, activation_clamp=clamp,
+                            unpacked_weights=unpacked)
+    assert np.array_equal(stats.cpu().numpy(), tr.routing.counts)
+    _stage_checks(buf, tr, s)
+    d = O.calc_diff(y.cpu(), tr.y)
+    log(f"  calc_diff={d:.3e}")
+    assert d <= CALC_DIFF_BAR
+
+
+def test_layer_schedules_agree_and_deterministic(mm, cuda, full_weights):
+    """Persistent (decode tiling) and staged (prefill tiling) accumulate every output element
+    in the same k order, so they must agree bitwise; repeated calls are bitwise identical."""
+    l1, l2 = full_weights[0], full_weights[1]
+    s = 200
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=99, global_experts=128)
+    buf = mm.SymmBuffer(None, 32, 384, 6, 4096, 2048)
+    log("schedules: staged")
+    y_staged = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    y_staged2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    log("schedules: persistent (dispatch_num_tokens=1)")
+    y_pers = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2, dispatch_num_tokens=1)
+    torch.cuda.synchronize()
+    assert torch.equal(y_staged, y_staged2)
+    assert torch.equal(y_staged, y_pers)
+
+
+def test_layer_zipf_empty_experts(mm, cuda, full_weights):
+    l1, l2, l1c, l2c, unpacked = full_weights
+    s = 512
+    log("layer zipf skew with empty experts")
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=4, routing="zipf")
+    buf = mm.SymmBuffer(None, 32, s, 6, 4096, 2048)
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, unpacked_weights=unpacked)
+    assert (tr.routing.counts == 0).sum() >= 4
+    d = O.calc_diff(y.cpu(), tr.y)
+    log(f"  calc_diff={d:.3e}")
+    assert d <= CALC_DIFF_BAR
+
+
+def test_layer_no_routed_rows(mm, cuda):
+    """Every slot invalid -> y == 0 exactly (no partial contributes)."""
+    s, e, hdim, inter = 10, 4, 256, 128
+    x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, 2, seed=1)
+    idx[:] = -1
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=2, mm=mm)
+    buf = mm.SymmBuffer(None, e, s, 2, hdim, inter)
+    log("layer with no routed rows")
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    assert torch.all(y.cpu() == 0)
+
+
+# ------------------------------------------------------------------ pre/post-process
+@pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
+def test_deepep_pre_post_process(mm, cuda, ids_dtype):
+    s, e, k, hdim = 300, 8, 4, 512
+    gen = torch.Generator().manual_seed(5)
+    x = (torch.randn((s, hdim), generator=gen)).to(torch.bfloat16)
+    x_fp8, x_sf = O.cast_to_fp8_channelwise(x)
+    idx = torch.randint(-1, e, (s, k), generator=gen).to(ids_dtype)
+    w = torch.rand((s, k), generator=gen)
+    ref = O.route(idx.to(torch.int64), torch.ones_like(w), e)  # preprocess ignores weights
+    counts = torch.from_numpy(ref.counts).to(torch.int32)
+    log(f"preprocess ids={ids_dtype}")
+    gx, gs, rw, mi, oi = mm.deepep_deepgemm_preprocess_channelwise(
+        x_fp8.to(cuda), x_sf.to(cuda), idx.to(cuda), w.to(cuda), counts.to(cuda), int(ref.num_rows))
+    torch.cuda.synchronize()
+    r = ref.num_rows
+    assert np.array_equal(oi.cpu().numpy(), ref.output_index)
+    assert np.array_equal(mi[:r].cpu().numpy(), ref.m_indices)
+    tok = torch.from_numpy(ref.row_token).long()
+    assert torch.equal(gx[:r].cpu().view(torch.uint8), x_fp8[tok].view(torch.uint8))
+    assert torch.equal(gs[:r].cpu(), x_sf[tok])
+    exp_w = w.reshape(-1)[torch.from_numpy(ref.row_token).long() * k
+                          + torch.from_numpy(ref.row_slot).long()]
+    assert torch.equal(rw[:r].cpu(), exp_w)
+    # postprocess: gather-sum of arbitrary l2_out rows, with and without weights
+    l2_out = (torch.randn((max(r, 1), hdim), generator=gen)).to(torch.bfloat16)
+    for apply_w in (False, True):
+        log(f"postprocess apply_w={apply_w}")
+        y = torch.empty((s, hdim), dtype=torch.bfloat16, device=cuda)
+        mm.deepep_deepgemm_postprocess_channelwise(y, l2_out.to(cuda), idx.to(cuda), w.to(cuda),
+                                                   oi, apply_topk_weights=apply_w)
+        torch.cuda.synchronize()
+        acc = torch.zeros((s, hdim))
+        oic = oi.cpu().long()
+        for j in range(k):
+            ok = (oic[:, j] >= 0) & (idx[:, j] >= 0)
+            v = l2_out.float()[oic[ok, j]]
+            if apply_w:
+                v = v * w[ok, j].view(-1, 1)
+            acc[ok] += v
+        assert torch.equal(y.cpu(), acc.to(torch.bfloat16))
