@@ -98,7 +98,7 @@ SIGNATURES = {
                                                + [ctypes.POINTER(c_i64)]),
     "mmoe_deepep_preprocess_channelwise": (
         ctypes.c_int,
-        [c_p] * 10 + [ctypes.c_int] * 7 + [c_p, c_i64, c_p]),
+        [c_p] * 10 + [ctypes.c_int] * 6 + [c_p, c_i64, c_p]),
     "mmoe_deepep_postprocess_channelwise": (
         ctypes.c_int, [c_p] * 5 + [ctypes.c_int] * 5 + [c_p]),
     "mmoe_cast_fp8_channelwise": (ctypes.c_int, [c_p, c_p, c_p, c_i64, c_i64, c_p]),

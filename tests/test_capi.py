@@ -18,6 +18,25 @@ def _header_functions():
     return sorted(set(re.findall(r"\b(mmoe_[a-z0-9_]+)\s*\(", src)))
 
 
+def _header_prototypes():
+    src = open(os.path.join(ROOT, "include", "megamoe_hip.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    protos = {}
+    for m in re.finditer(r"\b(mmoe_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", src):
+        params = [p.strip() for p in m.group(2).split(",") if p.strip()]
+        if params == ["void"]:
+            params = []
+        protos[m.group(1)] = params
+    return protos
+
+
+def test_bindings_match_header_arity():
+    protos = _header_prototypes()
+    assert set(protos) == set(_header_functions())
+    for name, params in protos.items():
+        assert len(_capi.SIGNATURES[name][1]) == len(params), name
+
+
 def test_library_exports_every_declared_symbol():
     lib = _capi.load()
     names = _header_functions()
