@@ -172,9 +172,12 @@ def main() -> int:
     counts = buf.scratch_view("counts").cpu()
     rows = int(counts.sum())
     touched = int((counts > 0).sum())
-    schedule = "staged" if mm._large_opt_3stage_selected(
-        s, buf._large_opt_3stage_mode, buf._large_opt_3stage_threshold) else "persistent"
-    log(f"routed rows R={rows}, touched experts={touched}, schedule={schedule}")
+    mode = buf._large_opt_3stage_mode
+    schedule = {"auto": "auto (per-expert engine)", "force": "tile engine",
+                "off": "streaming engine"}[mode]
+    stream_experts = int(((counts > 0) & (counts <= 64)).sum())
+    log(f"routed rows R={rows}, touched experts={touched}, schedule={schedule}, "
+        f"experts on the streaming engine={stream_experts if mode == 'auto' else '-'}")
 
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
@@ -193,7 +196,7 @@ def main() -> int:
 
     stage_ms = None
     if not args.no_stage_timing:
-        call = mm.LayerCall(y, l1, l2, buf, staged=(schedule == "staged"))
+        call = mm.LayerCall(y, l1, l2, buf)
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
         for i in range(args.steps):
             flush.fill_(i & 0x7f)

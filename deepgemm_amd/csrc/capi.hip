@@ -13,7 +13,7 @@ namespace {
 
 constexpr int kTokenAlignment = 384;  // deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:9
 constexpr int kMaxTopk = 16;
-constexpr int kDefaultThreshold = 128;  // megamoe/__init__.py:22
+constexpr int kMaxLayerExperts = 256;  // per-expert tile tables of the grouped GEMM
 
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
@@ -108,6 +108,7 @@ int validate_forward(const mmoe_forward_args* a) {
                         a->intermediate);
   if (st != MMOE_OK) return st;
   if (a->hidden % 16 || a->intermediate % 16) return MMOE_ERR_MARLIN_DIVISIBLE;
+  if (a->num_experts > kMaxLayerExperts) return MMOE_ERR_UNSUPPORTED_SHAPE;
   if (a->num_tokens < 0) return MMOE_ERR_ARGUMENT;
   if (a->num_tokens > a->num_max_tokens) return MMOE_ERR_TOO_MANY_TOKENS;
   if (!mmoe::gemm_shape_supported(2 * a->intermediate, a->hidden) ||
@@ -160,8 +161,7 @@ mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratc
 int run_route(const mmoe_forward_args* a, const mmoe_scratch_layout& l, hipStream_t s) {
   const mmoe::RouteArgs r = forward_route_args(a, l);
   const int64_t tasks = static_cast<int64_t>(a->num_tokens) * a->num_topk;
-  const int64_t chunks = (tasks + mmoe::kRouteChunk - 1) / mmoe::kRouteChunk;
-  return mmoe::launch_route(r, chunks, s) == hipSuccess ? MMOE_OK : MMOE_ERR_HIP;
+  return mmoe::launch_route(r, tasks, s) == hipSuccess ? MMOE_OK : MMOE_ERR_HIP;
 }
 
 }  // namespace
@@ -264,11 +264,11 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
                &l);
   auto runs = [&](int stage) { return first_stage <= stage && stage <= last_stage; };
 
-  const int threshold = a->token_threshold > 0 ? a->token_threshold : kDefaultThreshold;
-  bool staged = a->num_tokens > threshold;
-  if (a->schedule == MMOE_SCHEDULE_PERSISTENT) staged = false;
-  if (a->schedule == MMOE_SCHEDULE_STAGED) staged = true;
-  const mmoe::GemmShape shape = staged ? mmoe::GemmShape::kPrefill : mmoe::GemmShape::kDecode;
+  // AUTO: the engine is chosen per expert on the device from its routed rows (the row count is
+  // only known there); PERSISTENT / STAGED force the streaming / tiled engine for every expert.
+  const mmoe::GemmEngine engine = a->schedule == MMOE_SCHEDULE_PERSISTENT ? mmoe::GemmEngine::kStream
+                                  : a->schedule == MMOE_SCHEDULE_STAGED   ? mmoe::GemmEngine::kTile
+                                                                          : mmoe::GemmEngine::kAuto;
   const int max_rows = a->num_tokens * a->num_topk;
   void* ws = a->route_scratch;
 
@@ -290,8 +290,8 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   g1.num_experts = a->num_experts;
   g1.n = 2 * a->intermediate;
   g1.k = a->hidden;
-  if (runs(MMOE_STAGE_GEMM1) &&
-      mmoe::launch_grouped_gemm(g1, shape, max_rows, cus, s) != hipSuccess)
+  g1.engine = engine;
+  if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
   if (runs(MMOE_STAGE_SWIGLU)) {
@@ -318,7 +318,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     g2.c = at<uint16_t>(ws, l.part_offset);
     g2.n = a->hidden;
     g2.k = a->intermediate;
-    if (mmoe::launch_grouped_gemm(g2, shape, max_rows, cus, s) != hipSuccess) return MMOE_ERR_HIP;
+    if (mmoe::launch_grouped_gemm(g2, max_rows, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   }
 
   if (runs(MMOE_STAGE_COMBINE)) {
@@ -406,7 +406,7 @@ int mmoe_deepep_preprocess_channelwise(void* grouped_x, float* grouped_x_scale,
   r.row_weight = route_weights;
   r.m_indices = m_indices;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (mmoe::launch_route(r, chunks, s) != hipSuccess) return MMOE_ERR_HIP;
+  if (mmoe::launch_route(r, tasks, s) != hipSuccess) return MMOE_ERR_HIP;
   if (mmoe::launch_gather_tasks(static_cast<uint8_t*>(grouped_x), grouped_x_scale,
                                 static_cast<const uint8_t*>(recv_x), recv_x_scale, output_index,
                                 tasks, topk, hidden, s) != hipSuccess)

@@ -19,7 +19,7 @@ struct RouteArgs {
   int num_experts;
   int check_weight;               // forward rule: w != 0 required
   int64_t row_cap;                // rows >= row_cap are dropped (output_index = -1)
-  int32_t* chunk_counts;          // [nchunks, E] (becomes per-chunk bases after the scan)
+  int32_t* chunk_counts;          // [nchunks, E] per-chunk counts (large launches only)
   int32_t* counts;                // [E]
   int32_t* offsets;               // [E+1]
   int32_t* meta;                  // [16]; meta[0] = R
@@ -31,8 +31,13 @@ struct RouteArgs {
   int32_t* m_indices;             // [rows] or null
 };
 
-// Count -> scan -> stable scatter. Deterministic: rows of an expert in ascending task order.
-hipError_t launch_route(const RouteArgs& a, int64_t num_chunks, hipStream_t stream);
+// Count -> offsets -> stable scatter over at most max_tasks = S*K tasks. Deterministic: rows
+// of an expert in ascending task order. chunk_counts needs ceil(max_tasks/kRouteChunk)*E ints.
+hipError_t launch_route(const RouteArgs& a, int64_t max_tasks, hipStream_t stream);
+
+// Per-expert tile engine of the grouped GEMM: kAuto picks STREAM for experts with <= 64 rows
+// (weight streaming, decode) and TILE otherwise (128x128 MFMA tiles, prefill).
+enum class GemmEngine : int { kAuto = 0, kStream = 1, kTile = 2 };
 
 struct GemmArgs {
   const uint8_t* a;          // e4m3 rows, row-major, lda bytes apart
@@ -47,15 +52,13 @@ struct GemmArgs {
   int num_experts;
   int n;
   int k;
+  GemmEngine engine;
 };
 
-enum class GemmShape { kDecode, kPrefill };
-
 // Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
-// a_scale[r] * b_scale[e,n]). Persistent: the grid strides over (m-tile, n-tile) pairs
-// computed on device from counts.
-hipError_t launch_grouped_gemm(const GemmArgs& g, GemmShape shape, int max_rows, int num_cus,
-                               hipStream_t stream);
+// a_scale[r] * b_scale[e,n]). Persistent: the grid strides over the tiles, enumerated on the
+// device from counts (max_rows bounds the grid only).
+hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream);
 bool gemm_shape_supported(int n, int k);
 
 struct SwigluArgs {

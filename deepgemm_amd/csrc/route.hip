@@ -8,13 +8,15 @@
 // (mega_moe_baseline_hip.cu:75, mega_moe_dcu.cuh:359); here the order is the stable one --
 // ascending task index -- so counts, rows and output_index are bitwise reproducible.
 //
-// Three launches, all O(S*K) integer work, HBM-bound on the topk tables:
-//   1. count:   one workgroup per chunk of 1024 tasks, LDS histogram -> chunk_counts[c][e]
-//   2. scan:    one workgroup; per expert, exclusive scan over chunks (wave prefix sums),
-//               expert offsets, R, stats += counts
-//   3. scatter: one workgroup per chunk; stable rank of each task among equal experts via
-//               wave ballot/popcount (a match loop over the distinct experts of the wave)
-//               plus per-wave bases in LDS; writes output_index and the per-row tables.
+// Ranks come from wave ballots: for the distinct experts present in a 64-task wave slice
+// (a "match" loop over ballot masks) each lane's rank is the popcount of the equal-expert
+// lanes below it. Per-wave counts become per-wave bases through LDS prefix sums.
+//
+// Two launch shapes, both integer work bound by the topk tables' HBM reads:
+//   * small (<= 16384 tasks): ONE workgroup of 16 waves does count, scan and scatter;
+//   * large: a count kernel (one workgroup per chunk, LDS histogram) and a scatter kernel
+//     (one workgroup per chunk) that rebuilds the expert offsets and its chunk base from the
+//     per-chunk counts itself, so no grid-wide barrier or separate scan launch is needed.
 #include "common.cuh"
 #include "kernels.h"
 
@@ -22,163 +24,269 @@ namespace mmoe {
 
 namespace {
 
-constexpr int kRouteThreads = 256;
-constexpr int kRouteWaves = kRouteThreads / kWave;
-constexpr int kTasksPerWave = kRouteChunk / kRouteWaves;  // 256 contiguous tasks per wave
-constexpr int kScanThreads = 1024;
+constexpr int kSmallThreads = 1024;
+constexpr int kSmallWaves = kSmallThreads / kWave;
+constexpr int kSmallMaxExperts = 256;
+constexpr int kChunkThreads = 256;
+constexpr int kChunkWaves = kChunkThreads / kWave;
 
-__device__ __forceinline__ int task_expert(const RouteArgs& a, int64_t task) {
-  int64_t e = a.idx_i64 ? static_cast<const int64_t*>(a.topk_idx)[task]
-                        : static_cast<int64_t>(static_cast<const int32_t*>(a.topk_idx)[task]);
+// Expert of a task (or -1), from already-loaded id and weight.
+__device__ __forceinline__ int valid_expert(const RouteArgs& a, int64_t e, float w) {
   if (e < 0 || e >= a.num_experts) return -1;
-  if (a.check_weight && a.topk_w[task] == 0.0f) return -1;
+  if (a.check_weight && w == 0.0f) return -1;
   return static_cast<int>(e);
 }
 
-__global__ __launch_bounds__(kRouteThreads) void route_count_kernel(RouteArgs a) {
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int lane = lane_id();
+  return lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+}
+
+// Loads P passes of 64 tasks starting at `begin` (task begin + p*64 + lane) into registers,
+// all loads issued before any is used (one memory round trip per batch).
+template <int P>
+__device__ __forceinline__ void wave_load(const RouteArgs& a, int64_t begin, int64_t end, int* ev,
+                                          float* wv) {
+  const int lane = lane_id();
+  int64_t ids[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const int64_t task = begin + p * kWave + lane;
+    const bool ok = task < end;
+    const int64_t t = ok ? task : 0;
+    ids[p] = a.idx_i64 ? static_cast<const int64_t*>(a.topk_idx)[t]
+                       : static_cast<int64_t>(static_cast<const int32_t*>(a.topk_idx)[t]);
+    wv[p] = a.topk_w[t];
+    if (!ok) ids[p] = -1;
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p) ev[p] = valid_expert(a, ids[p], wv[p]);
+}
+
+// Adds the per-expert counts of one 64-task pass into cnt[e] (this wave's private row).
+__device__ __forceinline__ void wave_count_pass(int e, int* cnt) {
+  const int lane = lane_id();
+  uint64_t active = __ballot(e >= 0);
+  while (active != 0ull) {
+    const int leader = __ffsll(static_cast<unsigned long long>(active)) - 1;
+    const int le = __shfl(e, leader, kWave);
+    const uint64_t m = __ballot(e == le);
+    if (lane == leader) cnt[le] += __popcll(m);
+    __builtin_amdgcn_wave_barrier();
+    active &= ~m;
+  }
+}
+
+// Assigns rows to one 64-task pass in task order; base[e] is this wave's running base.
+__device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t task, bool in_range,
+                                                  int e, float w, int* base) {
+  const int lane = lane_id();
+  const uint64_t below = lanes_below();
+  int row = -1;
+  uint64_t active = __ballot(e >= 0);
+  while (active != 0ull) {
+    const int leader = __ffsll(static_cast<unsigned long long>(active)) - 1;
+    const int le = __shfl(e, leader, kWave);
+    const uint64_t m = __ballot(e == le);
+    const int b = base[le];
+    if (e == le) row = b + __popcll(m & below);
+    __builtin_amdgcn_wave_barrier();
+    if (lane == leader) base[le] = b + __popcll(m);
+    __builtin_amdgcn_wave_barrier();
+    active &= ~m;
+  }
+  if (row >= 0 && row >= a.row_cap) row = -1;
+  if (in_range) a.output_index[task] = row;
+  if (row >= 0) {
+    a.row_token[row] = static_cast<int32_t>(task / a.topk);
+    if (a.row_weight != nullptr) a.row_weight[row] = w;
+    if (a.m_indices != nullptr) a.m_indices[row] = e;
+  }
+}
+
+// Counts then scatters the tasks [begin, end) of this wave, in batches of kBatch passes held
+// in registers. `cnt` is the wave's count row (zeroed by the caller); between the two phases
+// the caller turns counts into bases (needs a workgroup barrier), passed through `phase_gap`.
+constexpr int kBatch = 8;
+
+template <class Gap>
+__device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* row,
+                           Gap phase_gap) {
+  int ev[kBatch];
+  float wv[kBatch];
+  for (int64_t b = begin; b < end; b += kBatch * kWave) {
+    wave_load<kBatch>(a, b, end, ev, wv);
+#pragma unroll
+    for (int p = 0; p < kBatch; ++p) wave_count_pass(ev[p], row);
+  }
+  phase_gap();
+  const int lane = lane_id();
+  for (int64_t b = begin; b < end; b += kBatch * kWave) {
+    wave_load<kBatch>(a, b, end, ev, wv);
+#pragma unroll
+    for (int p = 0; p < kBatch; ++p) {
+      const int64_t task = b + p * kWave + lane;
+      wave_scatter_pass(a, task, task < end, ev[p], wv[p], row);
+    }
+  }
+}
+
+// Expert offsets from totals (exclusive scan, or the caller's counts for the preprocess),
+// written by one thread; returns nothing, fills s_off[0..E].
+__device__ void publish_offsets(const RouteArgs& a, const int* s_tot, int* s_off, bool writer) {
+  if (threadIdx.x == 0) {
+    int64_t off = 0;
+    int64_t routed = 0;
+    for (int e = 0; e < a.num_experts; ++e) {
+      s_off[e] = static_cast<int>(off);
+      off += a.given_counts != nullptr ? a.given_counts[e] : s_tot[e];
+      routed += s_tot[e];
+    }
+    s_off[a.num_experts] = static_cast<int>(off);
+    if (writer) a.meta[0] = static_cast<int32_t>(routed < a.row_cap ? routed : a.row_cap);
+  }
+  __syncthreads();
+  if (writer) {
+    for (int e = threadIdx.x; e <= a.num_experts; e += blockDim.x) a.offsets[e] = s_off[e];
+    for (int e = threadIdx.x; e < a.num_experts; e += blockDim.x) {
+      a.counts[e] = s_tot[e];
+      if (a.stats != nullptr) a.stats[e] += s_tot[e];
+    }
+  }
+}
+
+__global__ __launch_bounds__(kSmallThreads) void route_small_kernel(RouteArgs a) {
+  __shared__ int s_cnt[kSmallWaves][kSmallMaxExperts];
+  __shared__ int s_tot[kSmallMaxExperts];
+  __shared__ int s_off[kSmallMaxExperts + 1];
+  const int wave = threadIdx.x / kWave;
+  const int E = a.num_experts;
+  const int64_t ntasks =
+      static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
+  const int64_t per = ((ntasks + kSmallWaves - 1) / kSmallWaves + kWave - 1) / kWave * kWave;
+  const int64_t begin = wave * per;
+  const int64_t end = begin + per < ntasks ? begin + per : ntasks;
+  for (int i = threadIdx.x; i < kSmallWaves * E; i += kSmallThreads) s_cnt[i / E][i % E] = 0;
+  __syncthreads();
+  wave_route(a, begin, end, s_cnt[wave], [&]() {
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += kSmallThreads) {
+      int run = 0;
+      for (int w = 0; w < kSmallWaves; ++w) {
+        const int c = s_cnt[w][e];
+        s_cnt[w][e] = run;
+        run += c;
+      }
+      s_tot[e] = run;
+    }
+    __syncthreads();
+    publish_offsets(a, s_tot, s_off, true);
+    for (int i = threadIdx.x; i < kSmallWaves * E; i += kSmallThreads) s_cnt[i / E][i % E] += s_off[i % E];
+    __syncthreads();
+  });
+}
+
+__global__ __launch_bounds__(kChunkThreads) void route_count_kernel(RouteArgs a, int chunk_tasks) {
   __shared__ int s_cnt[kMaxExperts];
   const int tid = threadIdx.x;
-  for (int e = tid; e < a.num_experts; e += kRouteThreads) s_cnt[e] = 0;
+  for (int e = tid; e < a.num_experts; e += kChunkThreads) s_cnt[e] = 0;
   __syncthreads();
-  const int64_t ntasks = static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kRouteChunk;
-  for (int i = tid; i < kRouteChunk; i += kRouteThreads) {
+  const int64_t ntasks =
+      static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * chunk_tasks;
+  for (int i = tid; i < chunk_tasks; i += kChunkThreads) {
     const int64_t task = base + i;
     if (task < ntasks) {
-      const int e = task_expert(a, task);
+      const int64_t id = a.idx_i64 ? static_cast<const int64_t*>(a.topk_idx)[task]
+                                   : static_cast<const int32_t*>(a.topk_idx)[task];
+      const int e = valid_expert(a, id, a.topk_w[task]);
       if (e >= 0) atomicAdd(&s_cnt[e], 1);
     }
   }
   __syncthreads();
   int32_t* dst = a.chunk_counts + static_cast<int64_t>(blockIdx.x) * a.num_experts;
-  for (int e = tid; e < a.num_experts; e += kRouteThreads) dst[e] = s_cnt[e];
+  for (int e = tid; e < a.num_experts; e += kChunkThreads) dst[e] = s_cnt[e];
 }
 
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int u = __shfl_up(v, off, kWave);
-    if (lane >= off) v += u;
-  }
-  return v;
-}
-
-__global__ __launch_bounds__(kScanThreads) void route_scan_kernel(RouteArgs a, int num_chunks) {
+__global__ __launch_bounds__(kChunkThreads) void route_chunk_scatter_kernel(RouteArgs a,
+                                                                            int chunk_tasks,
+                                                                            int num_chunks) {
+  __shared__ int s_wbase[kChunkWaves][kMaxExperts];
   __shared__ int s_tot[kMaxExperts];
-  const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  constexpr int waves = kScanThreads / kWave;
-  for (int e = wave; e < a.num_experts; e += waves) {
-    int carry = 0;
-    for (int c0 = 0; c0 < num_chunks; c0 += kWave) {
-      const int c = c0 + lane;
-      int32_t* p = a.chunk_counts + static_cast<int64_t>(c) * a.num_experts + e;
-      const int v = c < num_chunks ? *p : 0;
-      const int inc = wave_inclusive_scan(v);
-      if (c < num_chunks) *p = carry + inc - v;  // exclusive base of chunk c for expert e
-      carry += __shfl(inc, kWave - 1, kWave);
-    }
-    if (lane == 0) s_tot[e] = carry;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int64_t off = 0;
-    for (int e = 0; e < a.num_experts; ++e) {
-      a.offsets[e] = static_cast<int32_t>(off);
-      off += a.given_counts != nullptr ? a.given_counts[e] : s_tot[e];
-    }
-    a.offsets[a.num_experts] = static_cast<int32_t>(off);
-    int64_t routed = 0;
-    for (int e = 0; e < a.num_experts; ++e) routed += s_tot[e];
-    a.meta[0] = static_cast<int32_t>(routed < a.row_cap ? routed : a.row_cap);
-  }
-  for (int e = threadIdx.x; e < a.num_experts; e += kScanThreads) {
-    a.counts[e] = s_tot[e];
-    if (a.stats != nullptr) a.stats[e] += s_tot[e];
-  }
-}
-
-__global__ __launch_bounds__(kRouteThreads) void route_scatter_kernel(RouteArgs a) {
-  __shared__ int s_wbase[kRouteWaves][kMaxExperts];
+  __shared__ int s_off[kMaxExperts + 1];
+  __shared__ int s_cbase[kMaxExperts];
   const int tid = threadIdx.x;
-  const int lane = lane_id();
   const int wave = tid / kWave;
-  const int64_t ntasks = static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
-  const int64_t chunk_base = static_cast<int64_t>(blockIdx.x) * kRouteChunk;
-  const int64_t wave_base = chunk_base + static_cast<int64_t>(wave) * kTasksPerWave;
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-
-  // pass 1: per-wave counts per expert
-  for (int e = tid; e < kRouteWaves * a.num_experts; e += kRouteThreads)
-    s_wbase[e / a.num_experts][e % a.num_experts] = 0;
-  __syncthreads();
-  for (int p = 0; p < kTasksPerWave; p += kWave) {
-    const int64_t task = wave_base + p + lane;
-    const int e = task < ntasks ? task_expert(a, task) : -1;
-    uint64_t active = __ballot(e >= 0);
-    while (active != 0ull) {
-      const int leader = __ffsll(static_cast<unsigned long long>(active)) - 1;
-      const int le = __shfl(e, leader, kWave);
-      const uint64_t m = __ballot(e == le);
-      if (lane == leader) s_wbase[wave][le] += __popcll(m);
-      active &= ~m;
+  const int E = a.num_experts;
+  const int chunk = blockIdx.x;
+  // totals and this chunk's base per expert, from every chunk's counts
+  for (int e = tid; e < E; e += kChunkThreads) {
+    int tot0 = 0, tot1 = 0, base = 0;
+    int c = 0;
+    for (; c + 1 < num_chunks; c += 2) {
+      const int v0 = a.chunk_counts[static_cast<int64_t>(c) * E + e];
+      const int v1 = a.chunk_counts[static_cast<int64_t>(c + 1) * E + e];
+      tot0 += v0;
+      tot1 += v1;
+      base += (c < chunk ? v0 : 0) + (c + 1 < chunk ? v1 : 0);
     }
+    if (c < num_chunks) {
+      const int v0 = a.chunk_counts[static_cast<int64_t>(c) * E + e];
+      tot0 += v0;
+      base += c < chunk ? v0 : 0;
+    }
+    s_tot[e] = tot0 + tot1;
+    s_cbase[e] = base;
   }
   __syncthreads();
-  // per-wave bases: expert offset + chunk base + counts of the earlier waves of this chunk
-  const int32_t* cbase = a.chunk_counts + static_cast<int64_t>(blockIdx.x) * a.num_experts;
-  for (int e = tid; e < a.num_experts; e += kRouteThreads) {
-    int run = a.offsets[e] + cbase[e];
-    for (int w = 0; w < kRouteWaves; ++w) {
-      const int c = s_wbase[w][e];
-      s_wbase[w][e] = run;
-      run += c;
-    }
-  }
+  publish_offsets(a, s_tot, s_off, chunk == 0);
+  const int64_t ntasks =
+      static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
+  const int64_t cbegin = static_cast<int64_t>(chunk) * chunk_tasks;
+  const int64_t cend = cbegin + chunk_tasks < ntasks ? cbegin + chunk_tasks : ntasks;
+  const int64_t per = ((chunk_tasks / kChunkWaves) + kWave - 1) / kWave * kWave;
+  const int64_t begin = cbegin + wave * per < cend ? cbegin + wave * per : cend;
+  const int64_t end = begin + per < cend ? begin + per : cend;
+  for (int i = tid; i < kChunkWaves * E; i += kChunkThreads) s_wbase[i / E][i % E] = 0;
   __syncthreads();
-  // pass 2: stable ranks -> rows
-  for (int p = 0; p < kTasksPerWave; p += kWave) {
-    const int64_t task = wave_base + p + lane;
-    const bool in_range = task < ntasks;
-    const int e = in_range ? task_expert(a, task) : -1;
-    int row = -1;
-    uint64_t active = __ballot(e >= 0);
-    while (active != 0ull) {
-      const int leader = __ffsll(static_cast<unsigned long long>(active)) - 1;
-      const int le = __shfl(e, leader, kWave);
-      const uint64_t m = __ballot(e == le);
-      const int base = s_wbase[wave][le];
-      if (e == le) row = base + __popcll(m & lt_mask);
-      __builtin_amdgcn_wave_barrier();
-      if (lane == leader) s_wbase[wave][le] = base + __popcll(m);
-      __builtin_amdgcn_wave_barrier();
-      active &= ~m;
+  wave_route(a, begin, end, s_wbase[wave], [&]() {
+    __syncthreads();
+    for (int e = tid; e < E; e += kChunkThreads) {
+      int run = s_off[e] + s_cbase[e];
+      for (int w = 0; w < kChunkWaves; ++w) {
+        const int c = s_wbase[w][e];
+        s_wbase[w][e] = run;
+        run += c;
+      }
     }
-    if (row >= 0 && row >= a.row_cap) row = -1;
-    if (in_range) a.output_index[task] = row;
-    if (row >= 0) {
-      a.row_token[row] = static_cast<int32_t>(task / a.topk);
-      if (a.row_weight != nullptr) a.row_weight[row] = a.topk_w[task];
-      if (a.m_indices != nullptr) a.m_indices[row] = e;
-    }
-  }
+    __syncthreads();
+  });
 }
 
 }  // namespace
 
-hipError_t launch_route(const RouteArgs& a, int64_t num_chunks, hipStream_t stream) {
-  if (num_chunks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(route_count_kernel, dim3(static_cast<unsigned>(num_chunks)), dim3(kRouteThreads),
-                     0, stream, a);
+int64_t route_chunk_tasks(int64_t ntasks) {
+  // <= 256 chunks (one workgroup each), at least 1024 tasks per chunk, multiple of 1024
+  int64_t chunk = (ntasks + 255) / 256;
+  chunk = (chunk + kRouteChunk - 1) / kRouteChunk * kRouteChunk;
+  return chunk < kRouteChunk ? kRouteChunk : chunk;
+}
+
+hipError_t launch_route(const RouteArgs& a, int64_t max_tasks, hipStream_t stream) {
+  if (max_tasks <= 0) return hipSuccess;
+  if (max_tasks <= kSmallWaves * kRouteChunk && a.num_experts <= kSmallMaxExperts) {
+    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
+    return hipGetLastError();
+  }
+  const int64_t chunk = route_chunk_tasks(max_tasks);
+  const int64_t chunks = (max_tasks + chunk - 1) / chunk;
+  hipLaunchKernelGGL(route_count_kernel, dim3(static_cast<unsigned>(chunks)), dim3(kChunkThreads),
+                     0, stream, a, static_cast<int>(chunk));
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, a,
-                     static_cast<int>(num_chunks));
-  err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(route_scatter_kernel, dim3(static_cast<unsigned>(num_chunks)),
-                     dim3(kRouteThreads), 0, stream, a);
+  hipLaunchKernelGGL(route_chunk_scatter_kernel, dim3(static_cast<unsigned>(chunks)),
+                     dim3(kChunkThreads), 0, stream, a, static_cast<int>(chunk),
+                     static_cast<int>(chunks));
   return hipGetLastError();
 }
 

@@ -58,6 +58,16 @@ def _large_opt_3stage_selected(num_tokens: int, mode: str, threshold: int) -> bo
     return False
 
 
+def _schedule_for_mode(mode: str) -> int:
+    """auto -> per-expert engine choice on the device; force -> tile engine; off -> streaming
+    engine (see fp8_mega_moe)."""
+    if mode == "force":
+        return _capi.MMOE_SCHEDULE_STAGED
+    if mode == "off":
+        return _capi.MMOE_SCHEDULE_PERSISTENT
+    return _capi.MMOE_SCHEDULE_AUTO
+
+
 def _is_current_stream_capturing() -> bool:
     checker = getattr(torch.cuda, "is_current_stream_capturing", None)
     return bool(checker()) if checker is not None else False
@@ -153,7 +163,9 @@ def get_mega_moe_hip_build_config():
     config["large_opt_3stage_auto_values"] = sorted(_LARGE_OPT_AUTO_VALUES)
     config["large_opt_3stage_threshold_env"] = _LARGE_OPT_THRESHOLD_ENV
     config["large_opt_3stage_default_threshold"] = _LARGE_OPT_DEFAULT_THRESHOLD
-    config["large_opt_3stage_shape"] = "single GPU: any experts<=1024, topk<=16, H,I % 128 == 0"
+    config["large_opt_3stage_shape"] = "single GPU: experts<=256, topk<=16, H,I % 128 == 0"
+    config["large_opt_3stage_selection"] = ("auto: per expert on device (<=64 rows: streaming "
+                                            "engine, else 128x128 MFMA tiles)")
     config["cuda_graph_max_tokens_source"] = "requested num_max_tokens_per_rank"
     config["cuda_graph_execution"] = "explicit_big_fused_or_large_opt_3stage"
     return config
@@ -484,8 +496,7 @@ def _forward_args(y, l1_weights, l2_weights, stats, sym_buffer, activation_clamp
         num_tokens=y.size(0), num_max_tokens=sym_buffer.num_max_tokens_per_rank,
         num_experts=sym_buffer.num_experts, num_topk=sym_buffer.num_topk,
         hidden=sym_buffer.hidden, intermediate=sym_buffer.intermediate_hidden,
-        activation_clamp=clamp, schedule=schedule,
-        token_threshold=int(sym_buffer._large_opt_3stage_threshold))
+        activation_clamp=clamp, schedule=schedule, reserved=0)
     return args
 
 
@@ -509,9 +520,9 @@ class LayerCall:
         _validate_layer_tensors(y, l1_weights, l2_weights, stats, sym_buffer, (1, 1, 32),
                                 "swiglu")
         if staged is None:
-            staged = _large_opt_3stage_selected(y.size(0), sym_buffer._large_opt_3stage_mode,
-                                                sym_buffer._large_opt_3stage_threshold)
-        schedule = _capi.MMOE_SCHEDULE_STAGED if staged else _capi.MMOE_SCHEDULE_PERSISTENT
+            schedule = _schedule_for_mode(sym_buffer._large_opt_3stage_mode)
+        else:
+            schedule = _capi.MMOE_SCHEDULE_STAGED if staged else _capi.MMOE_SCHEDULE_PERSISTENT
         self._keep = (y, l1_weights, l2_weights, sym_buffer, stats)
         self.args = _forward_args(y, l1_weights, l2_weights, stats, sym_buffer,
                                   activation_clamp, schedule)
@@ -537,18 +548,19 @@ def fp8_mega_moe(
 ):
     """The layer; writes ``y`` in place and returns None (megamoe/__init__.py:328-449).
 
-    Schedules: the persistent small-T path and the staged large-T path of the reference map
-    to the decode- and prefill-shaped gfx950 GEMM tilings; the choice follows the reference's
-    env knobs and strict ``> threshold`` rule. Graph modes read the device token count
-    ``sym_buffer.cuda_graph_num_tokens`` at run time (a capturable launch sequence)."""
+    Schedules: the reference's persistent small-T kernel and staged large-T path become two
+    tile engines of one persistent grouped GEMM, chosen per expert on the device from its
+    routed rows (the row counts exist only there). ``MEGAMOE_DCU_USE_LARGE_OPT_3STAGE``
+    keeps its meaning: ``auto`` (default) = per-expert choice, ``1``/``3stage`` = tile engine
+    everywhere, ``0``/``off`` = streaming engine everywhere; every choice computes the same
+    layer. Flags, ``dispatch_num_tokens`` and graph-mode rules are validated exactly as in the
+    reference. Graph modes read the device token count ``sym_buffer.cuda_graph_num_tokens`` at
+    run time; the launch sequence allocates nothing and never synchronises, so it captures."""
     call_y = y
     if big_fused_cuda_graph and stages_fused_cuda_graph:
         raise ValueError("choose only one of big_fused_cuda_graph or stages_fused_cuda_graph")
     graph_mode = big_fused_cuda_graph or stages_fused_cuda_graph
     mode = getattr(sym_buffer, "_large_opt_3stage_mode", None) or _large_opt_3stage_mode()
-    threshold = getattr(sym_buffer, "_large_opt_3stage_threshold", None)
-    if threshold is None:
-        threshold = _large_opt_3stage_threshold()
     runtime_tokens = None
     if graph_mode:
         graph_max_tokens = int(sym_buffer.cuda_graph_max_tokens_per_rank)
@@ -565,8 +577,7 @@ def fp8_mega_moe(
                                "MEGAMOE_DCU_USE_LARGE_OPT_3STAGE=auto or 1")
         call_y = y[:graph_max_tokens] if capture_rows != graph_max_tokens else y
         runtime_tokens = sym_buffer.cuda_graph_num_tokens
-        schedule = _capi.MMOE_SCHEDULE_STAGED if stages_fused_cuda_graph else \
-            _capi.MMOE_SCHEDULE_PERSISTENT
+        schedule = _schedule_for_mode(mode)
     else:
         if _is_current_stream_capturing():
             raise RuntimeError(
@@ -578,8 +589,7 @@ def fp8_mega_moe(
         if dispatch_tokens < 0 or dispatch_tokens > int(sym_buffer.num_max_tokens_per_rank):
             raise ValueError("dispatch_num_tokens must be in "
                              f"0..{int(sym_buffer.num_max_tokens_per_rank)}")
-        staged = _large_opt_3stage_selected(dispatch_tokens, mode, threshold)
-        schedule = _capi.MMOE_SCHEDULE_STAGED if staged else _capi.MMOE_SCHEDULE_PERSISTENT
+        schedule = _schedule_for_mode(mode)
     _validate_layer_tensors(call_y, l1_weights, l2_weights, cumulative_local_expert_recv_stats,
                             sym_buffer, recipe, activation)
     _launch_layer(call_y, l1_weights, l2_weights, cumulative_local_expert_recv_stats, sym_buffer,

@@ -77,7 +77,7 @@ class ForwardArgs(ctypes.Structure):
         ("intermediate", c_i32),
         ("activation_clamp", ctypes.c_float),
         ("schedule", c_i32),
-        ("token_threshold", c_i32),
+        ("reserved", c_i32),
     ]
 
 

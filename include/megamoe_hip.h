@@ -48,10 +48,12 @@ extern "C" {
 #define MMOE_ERR_NO_DEVICE (-13)         /* no usable HIP device / not gfx950 */
 #define MMOE_ERR_ARGUMENT (-14)          /* other invalid argument */
 
-/* schedule override for mmoe_forward (the reference's MEGAMOE_DCU_USE_LARGE_OPT_3STAGE) */
-#define MMOE_SCHEDULE_AUTO 0       /* token threshold decides */
-#define MMOE_SCHEDULE_PERSISTENT 1 /* small-T, HBM-bound schedule */
-#define MMOE_SCHEDULE_STAGED 2     /* large-T, MFMA-bound schedule */
+/* Schedule of mmoe_forward (the reference's MEGAMOE_DCU_USE_LARGE_OPT_3STAGE auto/off/force).
+ * The grouped GEMMs have two tile engines; AUTO picks one per expert on the device from its
+ * routed row count (<= 64 rows: weight-streaming engine; more: 128x128 MFMA tile engine). */
+#define MMOE_SCHEDULE_AUTO 0       /* per-expert choice on the device */
+#define MMOE_SCHEDULE_PERSISTENT 1 /* streaming engine for every expert (HBM-bound decode) */
+#define MMOE_SCHEDULE_STAGED 2     /* tile engine for every expert (MFMA-bound prefill) */
 
 /* Byte layout of the per-GPU input buffer (the reference's sym_buffer).
  * Replaces get_symm_buffer_size_for_mega_moe and its slicer,
@@ -114,7 +116,7 @@ typedef struct mmoe_forward_args {
   int32_t intermediate;              /* I */
   float activation_clamp;            /* +inf = no clamp (reference: activation_clamp=None) */
   int32_t schedule;                  /* MMOE_SCHEDULE_* */
-  int32_t token_threshold;           /* staged when num_tokens > threshold (default 128) */
+  int32_t reserved;                  /* must be 0 */
 } mmoe_forward_args;
 
 /* get_token_alignment_for_mega_moe, csrc/apis/mega_dcu.hpp:24-26 (kTokenAlignment,

@@ -187,21 +187,28 @@ def test_layer_full_shape(mm, cuda, full_weights, case):
     assert d <= CALC_DIFF_BAR
 
 
-def test_layer_schedules_agree_and_deterministic(mm, cuda, full_weights):
-    """Persistent (decode tiling) and staged (prefill tiling) accumulate every output element
-    in the same k order, so they must agree bitwise; repeated calls are bitwise identical."""
-    l1, l2 = full_weights[0], full_weights[1]
-    s = 200
-    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=99, global_experts=128)
-    buf = mm.SymmBuffer(None, 32, 384, 6, 4096, 2048)
-    log("schedules: staged")
-    y_staged = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
-    y_staged2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
-    log("schedules: persistent (dispatch_num_tokens=1)")
-    y_pers = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2, dispatch_num_tokens=1)
+@pytest.mark.parametrize("mode", ["auto", "1", "0"])
+def test_layer_every_schedule_matches_oracle_and_is_deterministic(mm, cuda, full_weights,
+                                                                  monkeypatch, mode):
+    """MEGAMOE_DCU_USE_LARGE_OPT_3STAGE = auto (per-expert engine), 1 (tile engine everywhere),
+    0 (streaming engine everywhere): every schedule meets the bar on a mixed load (experts
+    with few and with many rows) and repeated calls are bitwise identical."""
+    l1, l2, l1c, l2c, unpacked = full_weights
+    s = 600
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=99, routing="zipf")
+    monkeypatch.setenv("MEGAMOE_DCU_USE_LARGE_OPT_3STAGE", mode)
+    buf = mm.SymmBuffer(None, 32, 768, 6, 4096, 2048)
+    log(f"schedule mode={mode}")
+    y1 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2).clone()
+    y2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
     torch.cuda.synchronize()
-    assert torch.equal(y_staged, y_staged2)
-    assert torch.equal(y_staged, y_pers)
+    assert torch.equal(y1, y2)
+    tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, unpacked_weights=unpacked)
+    counts = tr.routing.counts
+    assert (counts > 64).any() and ((counts > 0) & (counts <= 64)).any()
+    d = O.calc_diff(y1.cpu(), tr.y)
+    log(f"  calc_diff={d:.3e}")
+    assert d <= CALC_DIFF_BAR
 
 
 def test_layer_zipf_empty_experts(mm, cuda, full_weights):
@@ -230,6 +237,38 @@ def test_layer_no_routed_rows(mm, cuda):
     y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
     torch.cuda.synchronize()
     assert torch.all(y.cpu() == 0)
+
+
+# ------------------------------------------------------------------ graph-bucket mode
+@pytest.mark.parametrize("flag", ["big_fused_cuda_graph", "stages_fused_cuda_graph"])
+def test_graph_capture_replay_runtime_tokens(mm, cuda, flag):
+    """Capture once at the bucket size, replay with several device token counts: every replay
+    equals an eager call on that prefix (bitwise) and leaves rows past the prefix untouched."""
+    s_max, e, hdim, inter, k = 200, 8, 512, 256, 6
+    x_fp8, x_sf, idx, w = make_tokens(s_max, hdim, e, k, seed=21, global_experts=16)
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=22, mm=mm)
+    buf = mm.get_symm_buffer_for_mega_moe(None, e, s_max, k, hdim, inter)
+    for t, src in ((buf.x, x_fp8), (buf.x_sf, x_sf), (buf.topk_idx, idx), (buf.topk_weights, w)):
+        t[:s_max].copy_(src)
+    y = torch.zeros((s_max, hdim), dtype=torch.bfloat16, device=cuda)
+    log(f"graph mode {flag}: eager warm-up then capture")
+    mm.fp8_w8a8_mega_moe(y, l1, l2, buf, **{flag: True})
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, **{flag: True})
+    ref_buf = mm.SymmBuffer(None, e, s_max, k, hdim, inter)
+    for n in (s_max, 57, 1, 0, 133):
+        log(f"  replay with runtime tokens={n}")
+        y.fill_(7.0)
+        buf.cuda_graph_num_tokens.fill_(n)
+        graph.replay()
+        torch.cuda.synchronize()
+        if n > 0:
+            y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2)
+            torch.cuda.synchronize()
+            assert torch.equal(y[:n], y_ref), f"replay n={n}"
+        assert torch.all(y[n:] == 7.0), f"rows past the prefix were written (n={n})"
 
 
 # ------------------------------------------------------------------ pre/post-process
