@@ -53,7 +53,9 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->row_weight_offset = take(rows * 4);
   l->m_indices_offset = take(rows * 4);
   l->act_scale_offset = take(rows * 4);
-  l->h_offset = take(rows * 2 * intermediate * 2);
+  l->amax_offset = take(rows * 4);
+  l->done_offset = take(rows * 4);
+  l->y_offset = take(rows * static_cast<int64_t>(intermediate) * 4);
   l->act_offset = take(rows * static_cast<int64_t>(intermediate));
   l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
   l->total_bytes = off;
@@ -155,6 +157,8 @@ mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratc
   r.row_token = at<int32_t>(ws, l.row_token_offset);
   r.row_weight = at<float>(ws, l.row_weight_offset);
   r.m_indices = at<int32_t>(ws, l.m_indices_offset);
+  r.row_amax = at<uint32_t>(ws, l.amax_offset);
+  r.row_done = at<int32_t>(ws, l.done_offset);
   return r;
 }
 
@@ -278,37 +282,36 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   }
 
   mmoe::GemmArgs g1;
+  memset(&g1, 0, sizeof(g1));
   g1.a = static_cast<const uint8_t*>(a->x);
   g1.row_token = at<int32_t>(ws, l.row_token_offset);
   g1.a_scale = a->x_sf;
   g1.lda = a->hidden;
   g1.b = static_cast<const uint8_t*>(a->w1);
   g1.b_scale = a->w1_sf;
-  g1.c = at<uint16_t>(ws, l.h_offset);
+  g1.c = nullptr;
   g1.counts = at<int32_t>(ws, l.counts_offset);
   g1.offsets = at<int32_t>(ws, l.offsets_offset);
   g1.num_experts = a->num_experts;
   g1.n = 2 * a->intermediate;
   g1.k = a->hidden;
   g1.engine = engine;
+  g1.sw.enabled = 1;
+  g1.sw.inter = a->intermediate;
+  g1.sw.row_weight = at<float>(ws, l.row_weight_offset);
+  g1.sw.y = at<float>(ws, l.y_offset);
+  g1.sw.amax = at<uint32_t>(ws, l.amax_offset);
+  g1.sw.done = at<int32_t>(ws, l.done_offset);
+  g1.sw.act = at<uint8_t>(ws, l.act_offset);
+  g1.sw.act_scale = at<float>(ws, l.act_scale_offset);
+  g1.sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
+  g1.sw.clamp = a->activation_clamp;
   if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
-  if (runs(MMOE_STAGE_SWIGLU)) {
-    mmoe::SwigluArgs sw;
-    sw.h = at<uint16_t>(ws, l.h_offset);
-    sw.row_weight = at<float>(ws, l.row_weight_offset);
-    sw.meta = at<int32_t>(ws, l.meta_offset);
-    sw.act = at<uint8_t>(ws, l.act_offset);
-    sw.act_scale = at<float>(ws, l.act_scale_offset);
-    sw.inter = a->intermediate;
-    sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
-    sw.clamp = a->activation_clamp;
-    if (mmoe::launch_swiglu_quant(sw, max_rows, cus, s) != hipSuccess) return MMOE_ERR_HIP;
-  }
-
   if (runs(MMOE_STAGE_GEMM2)) {
     mmoe::GemmArgs g2 = g1;
+    memset(&g2.sw, 0, sizeof(g2.sw));
     g2.a = at<uint8_t>(ws, l.act_offset);
     g2.row_token = nullptr;
     g2.a_scale = at<float>(ws, l.act_scale_offset);

@@ -1,6 +1,4 @@
 // eltwise.hip -- the HBM-bound stages around the GEMMs (gfx950):
-//   * SwiGLU x route weight + per-row e4m3 requant (the reference's K2,
-//     megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:254-377), one wave per row;
 //   * the top-k combine as an inverse-index gather (no atomics, fixed slot order):
 //     y[t] = bf16(sum_s f32(part[output_index[t,s]])), the reference's reduce
 //     (deep_gemm/include/deep_gemm/impls/mega_moe_dcu.cuh:706-760) and baseline gather
@@ -15,66 +13,6 @@ namespace {
 
 constexpr int kEltThreads = 256;
 constexpr int kEltWaves = kEltThreads / kWave;
-
-// ---------------------------------------------------------------- SwiGLU + requant
-// Lane j of the wave owns 4-element groups j, j+64, ...; kGroups = ceil(I/4/64) per lane.
-template <int kGroups>
-__global__ __launch_bounds__(kEltThreads) void swiglu_quant_kernel(SwigluArgs s) {
-  const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  const int rows = s.meta[0];
-  const int inter = s.inter;
-  const int ngroups = inter >> 2;
-  for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
-    const float w = s.row_weight[row];
-    uint8_t* out = s.act + static_cast<int64_t>(row) * inter;
-    if (w == 0.0f) {
-      for (int gi = lane; gi < ngroups; gi += kWave) reinterpret_cast<uint32_t*>(out)[gi] = 0u;
-      if (lane == 0) s.act_scale[row] = kAmaxFloor / kE4m3Max;
-      continue;
-    }
-    const uint16_t* hrow = s.h + static_cast<int64_t>(row) * 2 * inter;
-    float y[kGroups][4];
-    float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kGroups; ++j) {
-      const int gi = lane + j * kWave;
-      if (gi < ngroups) {
-        const uint2 gv = *reinterpret_cast<const uint2*>(hrow + gi * 4);
-        const uint2 uv = *reinterpret_cast<const uint2*>(hrow + inter + gi * 4);
-        float gate[4] = {bf16_to_f32(gv.x & 0xffff), bf16_to_f32(gv.x >> 16),
-                         bf16_to_f32(gv.y & 0xffff), bf16_to_f32(gv.y >> 16)};
-        float up[4] = {bf16_to_f32(uv.x & 0xffff), bf16_to_f32(uv.x >> 16),
-                       bf16_to_f32(uv.y & 0xffff), bf16_to_f32(uv.y >> 16)};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float gq = gate[q], uq = up[q];
-          if (s.has_clamp) {
-            uq = fminf(s.clamp, fmaxf(-s.clamp, uq));
-            gq = fminf(s.clamp, gq);
-          }
-          const float v = gq * (1.0f / (1.0f + expf(-gq))) * uq * w;
-          y[j][q] = v;
-          amax = fmaxf(amax, fabsf(v));
-        }
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) y[j][q] = 0.0f;
-      }
-    }
-    amax = wave_max(amax);
-    const float a = fmaxf(amax, kAmaxFloor);
-    const float inv = kE4m3Max / a;
-    if (lane == 0) s.act_scale[row] = a / kE4m3Max;
-#pragma unroll
-    for (int j = 0; j < kGroups; ++j) {
-      const int gi = lane + j * kWave;
-      if (gi < ngroups)
-        reinterpret_cast<uint32_t*>(out)[gi] =
-            pack_e4m3x4(y[j][0] * inv, y[j][1] * inv, y[j][2] * inv, y[j][3] * inv);
-    }
-  }
-}
 
 // ---------------------------------------------------------------- combine
 // One workgroup per token (grid-stride); each thread owns 8-element (16-byte) columns.
@@ -233,23 +171,6 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 }
 
 }  // namespace
-
-hipError_t launch_swiglu_quant(const SwigluArgs& s, int64_t max_rows, int num_cus,
-                               hipStream_t stream) {
-  if (max_rows <= 0) return hipSuccess;
-  const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 8);
-  const int groups = (s.inter / 4 + kWave - 1) / kWave;
-  if (groups <= 2) {
-    hipLaunchKernelGGL(swiglu_quant_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, s);
-  } else if (groups <= 8) {
-    hipLaunchKernelGGL(swiglu_quant_kernel<8>, dim3(grid), dim3(kEltThreads), 0, stream, s);
-  } else if (groups <= 16) {
-    hipLaunchKernelGGL(swiglu_quant_kernel<16>, dim3(grid), dim3(kEltThreads), 0, stream, s);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
 
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream) {
   if (c.host_tokens <= 0) return hipSuccess;

@@ -1,27 +1,34 @@
-// gemm.hip -- grouped FP8 (OCP e4m3) GEMM on gfx950 MFMA for the expert-contiguous rows.
+// gemm.hip -- grouped FP8 (OCP e4m3) GEMMs of the layer on gfx950 MFMA, over the
+// expert-contiguous routed rows.
 //
-//   c[r, n] = bf16( (sum_k a[r,k] * b[e,n,k]) * a_scale[r] * b_scale[e,n] ),  e = expert of r
+// GEMM1 (gate+up, K = H) gathers its A rows straight from the token matrix through row_token
+// (the dispatch "pull" of the reference's K1, megamoe/dcu_megamoe_large_opt/K1_fused/
+// k1_fused_ext.cu:479-746), so no grouped copy of x exists, and fuses the K2 stage
+// (megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:254-377) into its epilogue:
+//   h = bf16(acc * x_sf[token] * w1_sf[e, n])       for the gate and the up column of a channel
+//   y = silu(min(h_g, c)) * clamp(h_u, -c, c) * w    (fp32, left to right)
+//   amax[row] = max |y| over the row (atomic max of the float bits: order-free, deterministic)
+// Each output tile holds matching gate and up channels, so SwiGLU is elementwise in registers.
+// The last tile to finish an M-tile (a per-M-tile counter) requantises its rows:
+//   a = max(amax, 1e-4); act = e4m3(clip(y * 448/a)); act_scale = a/448.
+// GEMM2 (down, K = I) reads act/act_scale and writes the bf16 partial rows for the combine:
+//   part[r, n] = bf16((sum_k act[r,k] * w2[e,n,k]) * act_scale[r] * w2_sf[e,n]).
 //
-// GEMM1 (gate+up, N = 2I, K = H) gathers its A rows straight from the token matrix through
-// row_token (the dispatch "pull" of the reference, K1: megamoe/dcu_megamoe_large_opt/K1_fused/
-// k1_fused_ext.cu:479-746), so no grouped copy of x is materialised. GEMM2 (N = H, K = I)
-// reads the requantised SwiGLU rows. B is the Marlin nt_kpack2 weight
-// (deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:50-66): per 16-row tile, each 16-byte
-// k-block of the 16 rows is 256 contiguous bytes.
+// B is the Marlin nt_kpack2 weight (deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:50-66):
+// per 16-row tile, each 16-byte k-block of the 16 rows is 256 contiguous bytes.
 //
-// One persistent kernel, two tile engines chosen per expert on the device from counts[]:
-//
-//  * STREAM engine (experts with <= 64 rows: decode). The layer is HBM-bound on the weights, so
-//    a tile is (expert, 64 output columns, all <= 64 rows) and its four waves split K four ways.
-//    Every wave loads its MFMA operands straight from global memory into registers (Marlin
-//    gives each lane 16 contiguous k-bytes of one weight row; 16 lanes read 256 contiguous
-//    bytes) through a 2-4 deep register ring, so 12-24 KB per wave is in flight with no LDS
-//    and no barrier in the K loop. The four K-partials are summed through LDS in a fixed order.
-//  * TILE engine (larger experts: prefill). 128x128 output tiles, BK = 128, A and B staged
-//    through double-buffered LDS in 16-row x 16-byte blocks (block (rb, kb) at
+// One persistent kernel per GEMM, two tile engines chosen per expert on the device from its
+// routed row count:
+//  * STREAM engine (<= 64 rows: decode, HBM-bound on the weights). Tile = (expert, 64 output
+//    columns, all rows). The four waves split K; each wave loads its MFMA operands straight from
+//    global memory into registers (Marlin gives each lane 16 contiguous k-bytes of one weight
+//    row; 16 lanes read 256 contiguous bytes) through a straight-line register ring 4 steps
+//    deep, with no LDS and no barrier in the K loop, one 32-row subtile at a time. The
+//    K-partials are summed through LDS in a fixed order.
+//  * TILE engine (more rows: prefill, MFMA-bound). 128x128 output tiles, BK = 128, A and B
+//    staged through double-buffered LDS in 16-row x 16-byte blocks (block (rb, kb) at
 //    (rb*BK/16 + kb)*256); a 32x32x64 MFMA operand of lane l (row l%32, k-half l/32) is two
 //    16-byte reads of consecutive blocks, 16 lanes reading 256 contiguous bytes (conflict-free).
-//
 // In both engines lane l supplies k-bytes [32*(l/32), 32*(l/32)+32) of each 64-k MFMA step for
 // A and B alike; any such bijection gives the same dot product.
 #include "common.cuh"
@@ -36,9 +43,7 @@ constexpr int kGemmWaves = kGemmThreads / kWave;
 constexpr int kMaxGemmExperts = 256;
 constexpr int kStreamMaxRows = 64;  // experts up to this many rows use the STREAM engine
 constexpr int kStreamBN = 64;
-// register ring depth (64-k steps in flight per wave): 4 with one 32-row subtile, 2 with two
-template <int MT>
-struct StreamDepth { static constexpr int value = MT == 1 ? 4 : 2; };
+constexpr int kStreamDepth = 4;     // register ring depth: 64-k steps in flight per wave
 constexpr int kTileBM = 128, kTileBN = 128, kTileBK = 128;
 constexpr int kTileWM = 2, kTileWN = 2;
 constexpr int kSmemBytes = 65536;
@@ -56,6 +61,8 @@ __device__ __forceinline__ v16f mfma_fp8(const v8i& a, const v8i& b, const v16f&
 
 __device__ __forceinline__ int4 ld16(const uint8_t* p) { return *reinterpret_cast<const int4*>(p); }
 
+__device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
 template <bool kGather>
 __device__ __forceinline__ float row_scale(const GemmArgs& g, int row) {
   return kGather ? g.a_scale[g.row_token[row]] : g.a_scale[row];
@@ -67,84 +74,122 @@ __device__ __forceinline__ const uint8_t* a_row_ptr(const GemmArgs& g, int row) 
   return g.a + src * g.lda;
 }
 
+// Weight row (output column of B) of column tile `ct` (32 columns) of n-block `nb`. With the
+// SwiGLU epilogue, tile nb holds gate channels [nb*W, nb*W+W) then the same up channels
+// (rows I + ...), W = columns per tile / 2.
+template <bool kSwiglu>
+__device__ __forceinline__ int weight_row(const GemmArgs& g, int nb, int tile_cols, int col) {
+  if (!kSwiglu) return nb * tile_cols + col;
+  const int half = tile_cols / 2;
+  return col < half ? nb * half + col : g.sw.inter + nb * half + (col - half);
+}
+
+// SwiGLU of one (row, channel): h rounded to bf16 exactly like the staged K1 output.
+__device__ __forceinline__ float swiglu_value(const GemmArgs& g, float gacc, float uacc, float xs,
+                                              float wsg, float wsu, float route_w) {
+  float gh = bf16_round(gacc * xs * wsg);
+  float uh = bf16_round(uacc * xs * wsu);
+  if (g.sw.has_clamp) {
+    uh = fminf(g.sw.clamp, fmaxf(-g.sw.clamp, uh));
+    gh = fminf(g.sw.clamp, gh);
+  }
+  return gh * (1.0f / (1.0f + expf(-gh))) * uh * route_w;
+}
+
+// max over the 32 lanes of each half-wave (the 32 channels of one output row)
+__device__ __forceinline__ float half_wave_max(float v) {
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+// The last of the `target` tiles of an M-tile requantises its rows [row0, row0+mrows).
+__device__ void finish_mtile(const GemmArgs& g, int row0, int mrows, int target) {
+  __shared__ int s_last;
+  __threadfence();  // release this workgroup's y stores and amax atomics
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = atomicAdd(g.sw.done + row0, 1) == target - 1;
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();  // acquire every other tile's y and amax
+  const int inter = g.sw.inter;
+  const int groups = inter >> 2;
+  for (int i = threadIdx.x; i < mrows * groups; i += kGemmThreads) {
+    const int r = i / groups;
+    const int q = i - r * groups;
+    const int row = row0 + r;
+    const float a = fmaxf(__uint_as_float(__atomic_load_n(g.sw.amax + row, __ATOMIC_RELAXED)),
+                          kAmaxFloor);
+    const float inv = kE4m3Max / a;
+    const float4 v = reinterpret_cast<const float4*>(g.sw.y + static_cast<int64_t>(row) * inter)[q];
+    reinterpret_cast<uint32_t*>(g.sw.act + static_cast<int64_t>(row) * inter)[q] =
+        pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+    if (q == 0) g.sw.act_scale[row] = a / kE4m3Max;
+  }
+}
+
 // ------------------------------------------------------------------ STREAM engine
-template <bool kGather, int MT>
-__device__ void stream_tile(const GemmArgs& g, int e, int row0, int mrows, int n0, uint8_t* smem) {
+// One 32-row subtile of a STREAM tile: the full K pass, the K-partial reduction and the epilogue.
+template <bool kGather, bool kSwiglu>
+__device__ void stream_subtile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
+  constexpr int kDepth = kStreamDepth;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int ksteps = g.k / 64;
   const int s_begin = wave * ksteps / kGemmWaves;
   const int nsteps = (wave + 1) * ksteps / kGemmWaves - s_begin;
-  const int khalf = (lane >> 5) * 32;
 
-  const uint8_t* ap[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = mt * 32 + (lane & 31);
-    ap[mt] = a_row_ptr<kGather>(g, row0 + (r < mrows ? r : 0)) + khalf + s_begin * 64;
-  }
+  const int r_lane = lane & 31;
+  const uint8_t* ap = a_row_ptr<kGather>(g, row0 + (r_lane < mrows ? r_lane : 0)) +
+                      (lane >> 5) * 32 + s_begin * 64;
   const uint8_t* bp[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
-    const int n = n0 + ct * 32 + (lane & 31);
+    const int n = weight_row<kSwiglu>(g, nb, kStreamBN, ct * 32 + (lane & 31));
     bp[ct] = g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) +
              (n & 15) * 16 + (lane >> 5) * 512 + static_cast<int64_t>(s_begin) * 1024;
   }
 
-  constexpr int kStreamDepth = StreamDepth<MT>::value;
-  int4 ar[kStreamDepth][MT][2];
-  int4 br[kStreamDepth][2][2];
+  int4 ar[kDepth][2];
+  int4 br[kDepth][2][2];
   auto issue = [&](int slot, int s) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      ar[slot][mt][0] = ld16(ap[mt] + s * 64);
-      ar[slot][mt][1] = ld16(ap[mt] + s * 64 + 16);
-    }
+    ar[slot][0] = ld16(ap + s * 64);
+    ar[slot][1] = ld16(ap + s * 64 + 16);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       br[slot][ct][0] = ld16(bp[ct] + static_cast<int64_t>(s) * 1024);
       br[slot][ct][1] = ld16(bp[ct] + static_cast<int64_t>(s) * 1024 + 256);
     }
   };
-
-  v16f acc[MT][2];
+  v16f acc[2];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[mt][ct][v] = 0.0f;
-
+    for (int v = 0; v < 16; ++v) acc[ct][v] = 0.0f;
   auto compute = [&](int slot) {
-    const v8i b0 = make_v8i(br[slot][0][0], br[slot][0][1]);
-    const v8i b1 = make_v8i(br[slot][1][0], br[slot][1][1]);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const v8i a = make_v8i(ar[slot][mt][0], ar[slot][mt][1]);
-      acc[mt][0] = mfma_fp8(a, b0, acc[mt][0]);
-      acc[mt][1] = mfma_fp8(a, b1, acc[mt][1]);
-    }
+    const v8i a = make_v8i(ar[slot][0], ar[slot][1]);
+    acc[0] = mfma_fp8(a, make_v8i(br[slot][0][0], br[slot][0][1]), acc[0]);
+    acc[1] = mfma_fp8(a, make_v8i(br[slot][1][0], br[slot][1][1]), acc[1]);
   };
-  if (nsteps >= kStreamDepth && nsteps % kStreamDepth == 0) {
-    // Straight-line ring: every load is unconditional, so the compiler's wait counts stay
-    // exact (each step waits only for its own slot, the oldest loads in flight).
-    // The scheduling barriers keep the issue order slot by slot, so a slot's loads are always
-    // the oldest in flight when it is consumed (wait = vmcnt of the younger slots).
+  if (nsteps >= kDepth && nsteps % kDepth == 0) {
+    // Straight-line ring: every load is unconditional and the scheduling barriers keep the
+    // issue order slot by slot, so a slot's loads are the oldest in flight when it is consumed
+    // (the compiler's wait = vmcnt of the younger slots).
 #pragma unroll
-    for (int d = 0; d < kStreamDepth; ++d) {
+    for (int d = 0; d < kDepth; ++d) {
       issue(d, d);
       __builtin_amdgcn_sched_barrier(0);
     }
-    for (int i = 0; i + kStreamDepth < nsteps; i += kStreamDepth) {
+    for (int i = 0; i + kDepth < nsteps; i += kDepth) {
 #pragma unroll
-      for (int d = 0; d < kStreamDepth; ++d) {
+      for (int d = 0; d < kDepth; ++d) {
         compute(d);
-        issue(d, i + d + kStreamDepth);
+        issue(d, i + d + kDepth);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
-    for (int d = 0; d < kStreamDepth; ++d) compute(d);
+    for (int d = 0; d < kDepth; ++d) compute(d);
   } else {
     // short or uneven K slices (small shapes): one step at a time
     for (int s = 0; s < nsteps; ++s) {
@@ -153,37 +198,72 @@ __device__ void stream_tile(const GemmArgs& g, int e, int row0, int mrows, int n
     }
   }
 
-  // fixed-order reduction of the four K partials: red[wave][mt][ct][v][lane]
+  // fixed-order reduction of the four K partials: red[wave][ct][v][lane]
   float* red = reinterpret_cast<float*>(smem);
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int v = 0; v < 16; ++v)
-        red[(((wave * 2 + mt) * 2 + ct) * 16 + v) * kWave + lane] = acc[mt][ct][v];
+    for (int v = 0; v < 16; ++v) red[((wave * 2 + ct) * 16 + v) * kWave + lane] = acc[ct][v];
   __syncthreads();
-  const int pmt = wave >> 1, pct = wave & 1;  // (mt, ct) pair this wave finishes
-  if (pmt < MT) {
-    const float bs = g.b_scale[static_cast<int64_t>(e) * g.n + n0 + pct * 32 + (lane & 31)];
-    uint16_t* cbase = g.c + n0 + pct * 32 + (lane & 31);
+  auto partial_sum = [&](int ct, int v) {
+    float s = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      float s = 0.0f;
+    for (int w = 0; w < kGemmWaves; ++w) s += red[((w * 2 + ct) * 16 + v) * kWave + lane];
+    return s;
+  };
+  // wave w finishes registers v in [4w, 4w+4) (rows 8*w + 4*(lane/32) + 0..3) of both columns
+  if (!kSwiglu) {
 #pragma unroll
-      for (int w = 0; w < kGemmWaves; ++w) s += red[(((w * 2 + pmt) * 2 + pct) * 16 + v) * kWave + lane];
-      const int r = pmt * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (r < mrows) {
-        const int row = row0 + r;
-        cbase[static_cast<int64_t>(row) * g.n] = f32_to_bf16(s * row_scale<kGather>(g, row) * bs);
+    for (int ct = 0; ct < 2; ++ct) {
+      const int col = nb * kStreamBN + ct * 32 + (lane & 31);
+      const float bs = g.b_scale[static_cast<int64_t>(e) * g.n + col];
+#pragma unroll
+      for (int vv = 0; vv < 4; ++vv) {
+        const int v = wave * 4 + vv;
+        const float s = partial_sum(ct, v);
+        const int r = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (r < mrows) {
+          const int row = row0 + r;
+          g.c[static_cast<int64_t>(row) * g.n + col] = f32_to_bf16(s * row_scale<kGather>(g, row) * bs);
+        }
       }
     }
+  } else {
+    const int chan = nb * (kStreamBN / 2) + (lane & 31);
+    const float wsg = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
+    const float wsu = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
+#pragma unroll
+    for (int vv = 0; vv < 4; ++vv) {
+      const int v = wave * 4 + vv;
+      const float ga = partial_sum(0, v);
+      const float ua = partial_sum(1, v);
+      const int r = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      float yv = 0.0f;
+      const bool ok = r < mrows;
+      const int row = row0 + (ok ? r : 0);
+      if (ok) {
+        yv = swiglu_value(g, ga, ua, row_scale<kGather>(g, row), wsg, wsu, g.sw.row_weight[row]);
+        g.sw.y[static_cast<int64_t>(row) * g.sw.inter + chan] = yv;
+      }
+      const float m = half_wave_max(fabsf(yv));
+      if (ok && (lane & 31) == 0) atomicMax(g.sw.amax + row, __float_as_uint(m));
+    }
   }
+  __syncthreads();  // the reduction buffer is reused by the next subtile / tile
+}
+
+// A STREAM tile: (expert, 64 columns, <= 64 rows) as one or two 32-row subtiles; the second
+// subtile re-reads the same weight slice, which the first left in L2.
+template <bool kGather, bool kSwiglu>
+__device__ void stream_tile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
+  for (int sub = 0; sub * 32 < mrows; ++sub)
+    stream_subtile<kGather, kSwiglu>(g, e, row0 + sub * 32, min(32, mrows - sub * 32), nb, smem);
+  if (kSwiglu) finish_mtile(g, row0, mrows, g.n / kStreamBN);
 }
 
 // ------------------------------------------------------------------ TILE engine
-template <bool kGather>
-__device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int n0, uint8_t* smem) {
+template <bool kGather, bool kSwiglu>
+__device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
   constexpr int BM = kTileBM, BN = kTileBN, BK = kTileBK;
   constexpr int KB = BK / 16;
   constexpr int kAPer = BM * BK / 16 / kGemmThreads;
@@ -212,7 +292,8 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int n0,
     const int c = tid + i * kGemmThreads;
     const int rb = c / (16 * KB);
     const int rem = c - rb * 16 * KB;
-    b_src[i] = g.b + (static_cast<int64_t>(e) * (g.n / 16) + n0 / 16 + rb) * (static_cast<int64_t>(g.k) * 16) + rem * 16;
+    const int n = weight_row<kSwiglu>(g, nb, BN, rb * 16);  // row-tile aligned
+    b_src[i] = g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) + rem * 16;
   }
   int4 ra[kAPer];
   int4 rbv[kBPer];
@@ -239,6 +320,10 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int n0,
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
+  // B tile column of the wave's column tile tn: without SwiGLU wn*64 + tn*32; with SwiGLU the
+  // wave's gate columns (tn = 0) sit at wn*32 and the matching up columns (tn = 1) at 64+wn*32.
+  auto b_col = [&](int tn) { return kSwiglu ? tn * (BN / 2) + wn * 32 : wn * WTN + tn * 32; };
+
   auto compute_stage = [&](int buf) {
     const uint8_t* sa = smem + buf * kStage;
     const uint8_t* sb = sa + BM * BK;
@@ -254,7 +339,7 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int n0,
       }
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
-        const int cidx = wn * WTN + tn * 32 + (lane & 31);
+        const int cidx = b_col(tn) + (lane & 31);
         const int off = ((cidx >> 4) * KB + kb) * 256 + (cidx & 15) * 16;
         bv[tn] = make_v8i(*reinterpret_cast<const int4*>(sb + off), *reinterpret_cast<const int4*>(sb + off + 256));
       }
@@ -276,28 +361,52 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int n0,
     __syncthreads();
   }
 
-  const float* bs = g.b_scale + static_cast<int64_t>(e) * g.n + n0;
+  if (!kSwiglu) {
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
+    for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int r = wm * WTM + tm * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      if (r < mrows) {
-        const int row = row0 + r;
-        const float sa = row_scale<kGather>(g, row);
-        uint16_t* crow = g.c + static_cast<int64_t>(row) * g.n + n0;
+      for (int v = 0; v < 16; ++v) {
+        const int r = wm * WTM + tm * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (r < mrows) {
+          const int row = row0 + r;
+          const float sa = row_scale<kGather>(g, row);
+          uint16_t* crow = g.c + static_cast<int64_t>(row) * g.n;
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-          const int col = wn * WTN + tn * 32 + (lane & 31);
-          crow[col] = f32_to_bf16(acc[tm][tn][v] * sa * bs[col]);
+          for (int tn = 0; tn < TN; ++tn) {
+            const int col = nb * BN + b_col(tn) + (lane & 31);
+            crow[col] = f32_to_bf16(acc[tm][tn][v] * sa * g.b_scale[static_cast<int64_t>(e) * g.n + col]);
+          }
         }
       }
     }
+  } else {
+    static_assert(TN == 2, "SwiGLU epilogue pairs one gate and one up column tile");
+    const int chan = nb * (BN / 2) + wn * 32 + (lane & 31);
+    const float wsg = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
+    const float wsu = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = wm * WTM + tm * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        const bool ok = r < mrows;
+        const int row = row0 + (ok ? r : 0);
+        float yv = 0.0f;
+        if (ok) {
+          yv = swiglu_value(g, acc[tm][0][v], acc[tm][1][v], row_scale<kGather>(g, row), wsg, wsu,
+                            g.sw.row_weight[row]);
+          g.sw.y[static_cast<int64_t>(row) * g.sw.inter + chan] = yv;
+        }
+        const float m = half_wave_max(fabsf(yv));
+        if (ok && (lane & 31) == 0) atomicMax(g.sw.amax + row, __float_as_uint(m));
+      }
+    }
+    finish_mtile(g, row0, mrows, g.n / kTileBN);
   }
 }
 
 // ------------------------------------------------------------------ persistent dispatcher
-template <bool kGather>
+template <bool kGather, bool kSwiglu>
 __global__ __launch_bounds__(kGemmThreads, 2) void grouped_gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_prefix[kMaxGemmExperts + 1];
@@ -343,17 +452,14 @@ __global__ __launch_bounds__(kGemmThreads, 2) void grouped_gemm_kernel(GemmArgs 
       const int nt = g.n / kTileBN;
       const int mt = local / nt;
       const int nb = local - mt * nt;
-      tile_tile<kGather>(g, e, g.offsets[e] + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM),
-                         nb * kTileBN, smem);
+      tile_tile<kGather, kSwiglu>(g, e, g.offsets[e] + mt * kTileBM,
+                                  min(kTileBM, cnt - mt * kTileBM), nb, smem);
     } else {
       const int nt = g.n / kStreamBN;
       const int mt = local / nt;
       const int nb = local - mt * nt;
-      const int mrows = min(kStreamMaxRows, cnt - mt * kStreamMaxRows);
-      if (mrows > 32)
-        stream_tile<kGather, 2>(g, e, g.offsets[e] + mt * kStreamMaxRows, mrows, nb * kStreamBN, smem);
-      else
-        stream_tile<kGather, 1>(g, e, g.offsets[e] + mt * kStreamMaxRows, mrows, nb * kStreamBN, smem);
+      stream_tile<kGather, kSwiglu>(g, e, g.offsets[e] + mt * kStreamMaxRows,
+                                    min(kStreamMaxRows, cnt - mt * kStreamMaxRows), nb, smem);
     }
     __syncthreads();
   }
@@ -374,11 +480,13 @@ hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hip
   int64_t grid = static_cast<int64_t>(num_cus) * 2;
   if (grid > stream_tiles) grid = stream_tiles;
   if (grid < 1) grid = 1;
-  if (g.row_token != nullptr) {
-    hipLaunchKernelGGL(grouped_gemm_kernel<true>, dim3(static_cast<unsigned>(grid)),
+  if (g.sw.enabled) {
+    if (g.row_token == nullptr || g.n != 2 * g.sw.inter) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), dim3(static_cast<unsigned>(grid)),
                        dim3(kGemmThreads), kSmemBytes, stream, g);
   } else {
-    hipLaunchKernelGGL(grouped_gemm_kernel<false>, dim3(static_cast<unsigned>(grid)),
+    if (g.row_token != nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), dim3(static_cast<unsigned>(grid)),
                        dim3(kGemmThreads), kSmemBytes, stream, g);
   }
   return hipGetLastError();

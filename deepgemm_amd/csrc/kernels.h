@@ -29,6 +29,8 @@ struct RouteArgs {
   int32_t* row_token;             // [rows]
   float* row_weight;              // [rows] or null
   int32_t* m_indices;             // [rows] or null
+  uint32_t* row_amax;             // [rows] or null: per-row |y| max of the fused GEMM1, cleared here
+  int32_t* row_done;              // [rows] or null: per-M-tile completion counters, cleared here
 };
 
 // Count -> offsets -> stable scatter over at most max_tasks = S*K tasks. Deterministic: rows
@@ -38,6 +40,20 @@ hipError_t launch_route(const RouteArgs& a, int64_t max_tasks, hipStream_t strea
 // Per-expert tile engine of the grouped GEMM: kAuto picks STREAM for experts with <= 64 rows
 // (weight streaming, decode) and TILE otherwise (128x128 MFMA tiles, prefill).
 enum class GemmEngine : int { kAuto = 0, kStream = 1, kTile = 2 };
+
+// Fused GEMM1 epilogue: SwiGLU x route weight, fp32 y, per-row |y| max, per-M-tile requant.
+struct SwigluEpilogue {
+  int enabled;
+  int inter;                // I: gate weight rows [0, I), up rows [I, 2I)
+  const float* row_weight;  // [rows] top-k weight of each routed row
+  float* y;                 // f32 [rows, I] SwiGLU output (before requant)
+  uint32_t* amax;           // [rows] float bits of max |y| (atomic max; cleared by the route)
+  int32_t* done;            // [rows] finished-tile counter of the M-tile starting at that row
+  uint8_t* act;             // e4m3 [rows, I] requantised y (GEMM2's A)
+  float* act_scale;         // [rows]
+  int has_clamp;
+  float clamp;
+};
 
 struct GemmArgs {
   const uint8_t* a;          // e4m3 rows, row-major, lda bytes apart
@@ -53,6 +69,7 @@ struct GemmArgs {
   int n;
   int k;
   GemmEngine engine;
+  SwigluEpilogue sw;         // GEMM1 only (requires row_token); c is unused then
 };
 
 // Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
@@ -60,19 +77,6 @@ struct GemmArgs {
 // device from counts (max_rows bounds the grid only).
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream);
 bool gemm_shape_supported(int n, int k);
-
-struct SwigluArgs {
-  const uint16_t* h;          // bf16 [rows, 2I]
-  const float* row_weight;    // [rows]
-  const int32_t* meta;        // meta[0] = rows
-  uint8_t* act;               // e4m3 [rows, I]
-  float* act_scale;           // [rows]
-  int inter;
-  int has_clamp;
-  float clamp;
-};
-hipError_t launch_swiglu_quant(const SwigluArgs& s, int64_t max_rows, int num_cus,
-                               hipStream_t stream);
 
 struct CombineArgs {
   uint16_t* y;                     // bf16 [S, H]

@@ -8,9 +8,10 @@
 // (mega_moe_baseline_hip.cu:75, mega_moe_dcu.cuh:359); here the order is the stable one --
 // ascending task index -- so counts, rows and output_index are bitwise reproducible.
 //
-// Ranks come from wave ballots: for the distinct experts present in a 64-task wave slice
-// (a "match" loop over ballot masks) each lane's rank is the popcount of the equal-expert
-// lanes below it. Per-wave counts become per-wave bases through LDS prefix sums.
+// Ranks come from wave ballots: one ballot per bit of the expert id gives every lane the mask
+// of lanes holding the same expert (a match-any in log2(E) votes); a lane's rank is the
+// popcount of that mask below it and the group's lowest lane publishes the group size. Per-wave
+// counts become per-wave bases through LDS prefix sums.
 //
 // Two launch shapes, both integer work bound by the topk tables' HBM reads:
 //   * small (<= 16384 tasks): ONE workgroup of 16 waves does count, scan and scatter;
@@ -63,44 +64,43 @@ __device__ __forceinline__ void wave_load(const RouteArgs& a, int64_t begin, int
   for (int p = 0; p < P; ++p) ev[p] = valid_expert(a, ids[p], wv[p]);
 }
 
-// Adds the per-expert counts of one 64-task pass into cnt[e] (this wave's private row).
-__device__ __forceinline__ void wave_count_pass(int e, int* cnt) {
-  const int lane = lane_id();
-  uint64_t active = __ballot(e >= 0);
-  while (active != 0ull) {
-    const int leader = __ffsll(static_cast<unsigned long long>(active)) - 1;
-    const int le = __shfl(e, leader, kWave);
-    const uint64_t m = __ballot(e == le);
-    if (lane == leader) cnt[le] += __popcll(m);
-    __builtin_amdgcn_wave_barrier();
-    active &= ~m;
+// Lanes of the wave holding the same expert id as this lane (invalid lanes: none), from one
+// ballot per id bit: O(log2 E) wave votes, no loop over the distinct experts.
+__device__ __forceinline__ uint64_t match_expert(int e, int id_bits) {
+  const uint64_t valid = __ballot(e >= 0);
+  uint64_t m = valid;
+  for (int b = 0; b < id_bits; ++b) {
+    const uint64_t ones = __ballot(e >= 0 && ((e >> b) & 1));
+    m &= ((e >> b) & 1) ? ones : ~ones;
   }
+  return e >= 0 ? m : 0ull;
+}
+
+// Adds the per-expert counts of one 64-task pass into cnt[e] (this wave's private row): the
+// lowest lane of every equal-expert group adds the group size.
+__device__ __forceinline__ void wave_count_pass(int e, int id_bits, int* cnt) {
+  const uint64_t m = match_expert(e, id_bits);
+  if (e >= 0 && (m & lanes_below()) == 0ull) cnt[e] += __popcll(m);
+  __builtin_amdgcn_wave_barrier();
 }
 
 // Assigns rows to one 64-task pass in task order; base[e] is this wave's running base.
 __device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t task, bool in_range,
-                                                  int e, float w, int* base) {
-  const int lane = lane_id();
-  const uint64_t below = lanes_below();
+                                                  int e, float w, int id_bits, int* base) {
+  const uint64_t m = match_expert(e, id_bits);
   int row = -1;
-  uint64_t active = __ballot(e >= 0);
-  while (active != 0ull) {
-    const int leader = __ffsll(static_cast<unsigned long long>(active)) - 1;
-    const int le = __shfl(e, leader, kWave);
-    const uint64_t m = __ballot(e == le);
-    const int b = base[le];
-    if (e == le) row = b + __popcll(m & below);
-    __builtin_amdgcn_wave_barrier();
-    if (lane == leader) base[le] = b + __popcll(m);
-    __builtin_amdgcn_wave_barrier();
-    active &= ~m;
-  }
+  if (e >= 0) row = base[e] + __popcll(m & lanes_below());
+  __builtin_amdgcn_wave_barrier();
+  if (e >= 0 && (m & lanes_below()) == 0ull) base[e] += __popcll(m);
+  __builtin_amdgcn_wave_barrier();
   if (row >= 0 && row >= a.row_cap) row = -1;
   if (in_range) a.output_index[task] = row;
   if (row >= 0) {
     a.row_token[row] = static_cast<int32_t>(task / a.topk);
     if (a.row_weight != nullptr) a.row_weight[row] = w;
     if (a.m_indices != nullptr) a.m_indices[row] = e;
+    if (a.row_amax != nullptr) a.row_amax[row] = 0u;
+    if (a.row_done != nullptr) a.row_done[row] = 0;
   }
 }
 
@@ -114,10 +114,12 @@ __device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* 
                            Gap phase_gap) {
   int ev[kBatch];
   float wv[kBatch];
+  int id_bits = 0;
+  while ((1 << id_bits) < a.num_experts) ++id_bits;
   for (int64_t b = begin; b < end; b += kBatch * kWave) {
     wave_load<kBatch>(a, b, end, ev, wv);
 #pragma unroll
-    for (int p = 0; p < kBatch; ++p) wave_count_pass(ev[p], row);
+    for (int p = 0; p < kBatch; ++p) wave_count_pass(ev[p], id_bits, row);
   }
   phase_gap();
   const int lane = lane_id();
@@ -126,7 +128,7 @@ __device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* 
 #pragma unroll
     for (int p = 0; p < kBatch; ++p) {
       const int64_t task = b + p * kWave + lane;
-      wave_scatter_pass(a, task, task < end, ev[p], wv[p], row);
+      wave_scatter_pass(a, task, task < end, ev[p], wv[p], id_bits, row);
     }
   }
 }

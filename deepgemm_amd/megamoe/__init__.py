@@ -274,7 +274,8 @@ class SymmBuffer:
     # -- stage-parity views into route_scratch (debug; valid after a call) --
     def scratch_view(self, name: str, num_rows: Optional[int] = None) -> torch.Tensor:
         """Intermediate tensors of the last call: counts, offsets, meta, output_index,
-        row_token, row_weight, m_indices, act_scale, h, act, part."""
+        row_token, row_weight, m_indices, act_scale, amax (max |y| per row), y (SwiGLU x
+        weight, f32), act (requantised y), part (GEMM2 rows)."""
         l = self.scratch_layout
         e, t, k = self.num_experts, self.num_max_tokens_per_rank, self.num_topk
         rows = int(l.row_capacity if num_rows is None else num_rows)
@@ -287,7 +288,8 @@ class SymmBuffer:
             "row_weight": (l.row_weight_offset, torch.float32, (rows,)),
             "m_indices": (l.m_indices_offset, torch.int32, (rows,)),
             "act_scale": (l.act_scale_offset, torch.float32, (rows,)),
-            "h": (l.h_offset, torch.bfloat16, (rows, 2 * self.intermediate_hidden)),
+            "amax": (l.amax_offset, torch.float32, (rows,)),
+            "y": (l.y_offset, torch.float32, (rows, self.intermediate_hidden)),
             "act": (l.act_offset, torch.float8_e4m3fn, (rows, self.intermediate_hidden)),
             "part": (l.part_offset, torch.bfloat16, (rows, self.hidden)),
         }
@@ -511,9 +513,9 @@ def _launch_layer(y, l1_weights, l2_weights, stats, sym_buffer, activation_clamp
 class LayerCall:
     """A prepared layer call whose stages can be launched one at a time (profiling, stage
     parity). ``run(first, last)`` launches stages [first, last] on the current stream:
-    0 route, 1 GEMM1, 2 SwiGLU+requant, 3 GEMM2, 4 combine."""
+    0 route, 1 GEMM1 with the fused SwiGLU + requant, 2 GEMM2, 3 combine."""
 
-    STAGES = ("route", "gemm1", "swiglu_quant", "gemm2", "combine")
+    STAGES = ("route", "gemm1_swiglu_quant", "gemm2", "combine")
 
     def __init__(self, y, l1_weights, l2_weights, sym_buffer, activation_clamp=None,
                  staged: Optional[bool] = None, stats=None):
@@ -527,7 +529,7 @@ class LayerCall:
         self.args = _forward_args(y, l1_weights, l2_weights, stats, sym_buffer,
                                   activation_clamp, schedule)
 
-    def run(self, first: int = 0, last: int = 4) -> None:
+    def run(self, first: int = 0, last: int = 3) -> None:
         _capi.check(_capi.load().mmoe_forward_stages(ctypes.byref(self.args), first, last,
                                                      _stream_handle()), "fp8_mega_moe")
 

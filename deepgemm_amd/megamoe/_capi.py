@@ -47,7 +47,9 @@ class ScratchLayout(ctypes.Structure):
         ("row_weight_offset", c_i64),
         ("m_indices_offset", c_i64),
         ("act_scale_offset", c_i64),
-        ("h_offset", c_i64),
+        ("amax_offset", c_i64),
+        ("done_offset", c_i64),
+        ("y_offset", c_i64),
         ("act_offset", c_i64),
         ("part_offset", c_i64),
     ]

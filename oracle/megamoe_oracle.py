@@ -224,14 +224,11 @@ def grouped_gemm_dequant(a_fp8: torch.Tensor, a_scale: torch.Tensor, w_fp8: torc
     return out
 
 
-def swiglu_quant_k2(h: torch.Tensor, route_weight: torch.Tensor,
-                    clamp: Optional[float]) -> Tuple[torch.Tensor, torch.Tensor]:
-    """K2: megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:254-377.
-    g = min(h_gate, c); u = clamp(h_up, -c, c); y = g*(1/(1+exp(-g)))*u*w (fp32, left to
-    right); a = max(max|y|, 1e-4); q = e4m3(clip(y*(448/a))); scale = a/448.
-    Rows with w == 0 -> q = 0 and scale = 1e-4/448."""
-    rows, two_i = h.shape
-    inter = two_i // 2
+def swiglu_k2(h: torch.Tensor, route_weight: torch.Tensor, clamp: Optional[float]) -> torch.Tensor:
+    """The fp32 SwiGLU x route weight of K2 (megamoe/dcu_megamoe_large_opt/K2_fused/
+    k2_fused_ext.cu:283-340): g = min(h_gate, c); u = clamp(h_up, -c, c);
+    y = g*(1/(1+exp(-g)))*u*w, left to right."""
+    inter = h.shape[1] // 2
     g = h[:, :inter].float()
     u = h[:, inter:].float()
     if clamp is not None and math.isfinite(clamp):
@@ -239,7 +236,17 @@ def swiglu_quant_k2(h: torch.Tensor, route_weight: torch.Tensor,
         u = torch.clamp(u, -c, c)
         g = torch.clamp(g, max=c)
     w = route_weight.float().view(-1, 1)
-    y = g * (1.0 / (1.0 + torch.exp(-g))) * u * w
+    return g * (1.0 / (1.0 + torch.exp(-g))) * u * w
+
+
+def swiglu_quant_k2(h: torch.Tensor, route_weight: torch.Tensor,
+                    clamp: Optional[float]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """K2: megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:254-377.
+    y = swiglu_k2(h, w, c); a = max(max|y|, 1e-4); q = e4m3(clip(y*(448/a))); scale = a/448.
+    Rows with w == 0 -> q = 0 and scale = 1e-4/448."""
+    rows, two_i = h.shape
+    inter = two_i // 2
+    y = swiglu_k2(h, route_weight, clamp)
     amax = y.abs().amax(dim=1) if inter > 0 else torch.zeros(rows)
     a = torch.clamp(amax, min=AMAX_FLOOR)
     inv = (E4M3_MAX / a).view(-1, 1)
@@ -274,6 +281,7 @@ def combine(part: torch.Tensor, output_index, num_tokens: int) -> torch.Tensor:
 class ForwardTrace:
     routing: Routing
     h: torch.Tensor
+    y_act: torch.Tensor
     act: torch.Tensor
     act_scale: torch.Tensor
     part: torch.Tensor
@@ -312,10 +320,11 @@ def mega_moe_forward(x_fp8: torch.Tensor, x_sf: torch.Tensor, topk_idx, topk_wei
     a = x_fp8[:s].cpu()[tok]
     a_s = x_sf[:s].cpu()[tok]
     h = grouped_gemm_dequant(a, a_s, w1, sw1.cpu(), rt.m_indices, rt.offsets)
-    act, act_s = swiglu_quant_k2(h, torch.as_tensor(rt.row_weight), activation_clamp)
+    rw = torch.as_tensor(rt.row_weight)
+    act, act_s = swiglu_quant_k2(h, rw, activation_clamp)
     part = grouped_gemm_dequant(act, act_s, w2, sw2.cpu(), rt.m_indices, rt.offsets)
     y = combine(part, rt.output_index, s)
-    return ForwardTrace(rt, h, act, act_s, part, y)
+    return ForwardTrace(rt, h, swiglu_k2(h, rw, activation_clamp), act, act_s, part, y)
 
 
 # ----------------------------------------------------------------------------------------

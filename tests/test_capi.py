@@ -95,7 +95,8 @@ def test_layouts():
     assert lay.row_capacity >= 384 * 6
     offs = [lay.counts_offset, lay.offsets_offset, lay.meta_offset, lay.chunk_counts_offset,
             lay.output_index_offset, lay.row_token_offset, lay.row_weight_offset,
-            lay.m_indices_offset, lay.act_scale_offset, lay.h_offset, lay.act_offset,
+            lay.m_indices_offset, lay.act_scale_offset, lay.amax_offset, lay.done_offset,
+            lay.y_offset, lay.act_offset,
             lay.part_offset]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert lay.part_offset + lay.row_capacity * 4096 * 2 <= lay.total_bytes
@@ -117,7 +118,7 @@ def test_layout_validation_codes(args, code):
 
 def _args(**kw):
     base = dict(num_tokens=4, num_max_tokens=384, num_experts=32, num_topk=6, hidden=4096,
-                intermediate=2048, activation_clamp=math.inf, schedule=0, token_threshold=128,
+                intermediate=2048, activation_clamp=math.inf, schedule=0, reserved=0,
                 route_scratch_bytes=1 << 40, sym_buffer_bytes=1 << 40)
     base.update(kw)
     a = _capi.ForwardArgs()

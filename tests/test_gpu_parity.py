@@ -116,9 +116,16 @@ def test_routing_bit_exact(mm, cuda, name):
 # ------------------------------------------------------------------ the layer
 def _stage_checks(buf, tr, s):
     r = tr.routing.num_rows
-    h = buf.scratch_view("h")[:r].cpu()
-    assert O.calc_diff(h, tr.h) < 1e-5, "GEMM1 (gate||up) output"
+    y_act = buf.scratch_view("y")[:r].cpu()
+    assert O.calc_diff(y_act, tr.y_act) < 1e-5, "GEMM1 + SwiGLU x weight output"
+    amax = buf.scratch_view("amax")[:r].cpu()
+    assert torch.allclose(amax, y_act.abs().amax(dim=1)), "row max |y| (atomic max)"
     act_s = buf.scratch_view("act_scale")[:r].cpu()
+    assert torch.equal(act_s, torch.clamp(amax, min=1e-4) / 448.0), "act_scale from amax"
+    # requant is exact given y: e4m3(clip(y * 448/a))
+    requant = O.e4m3_from_f32(y_act * (448.0 / torch.clamp(amax, min=1e-4)).view(-1, 1))
+    assert torch.equal(buf.scratch_view("act")[:r].cpu().view(torch.uint8),
+                       requant.view(torch.uint8)), "per-row requant"
     assert torch.allclose(act_s, tr.act_scale, rtol=2e-2, atol=0)
     act = buf.scratch_view("act")[:r].cpu()
     deq = act.float() * act_s.view(-1, 1)
