@@ -59,6 +59,15 @@ def calc_diff(x: torch.Tensor, y: torch.Tensor) -> float:
 # ----------------------------------------------------------------------------------------
 # quantisation helpers (megamoe/__init__.py:51-98)
 # ----------------------------------------------------------------------------------------
+def fdiv(num: float, den: torch.Tensor) -> torch.Tensor:
+    """Correctly rounded fp32 num/den. (torch evaluates ``scalar / tensor`` as
+    ``reciprocal(tensor) * scalar``, which is off by 1 ulp now and then; the reference's
+    kernels divide in fp32, e.g. ``448.0f / clamped_amax`` in
+    megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:352.)"""
+    den = den.float()
+    return torch.div(torch.full_like(den, float(num)), den)
+
+
 def e4m3_from_f32(v: torch.Tensor) -> torch.Tensor:
     """Clip to +-448 then round-to-nearest-even into e4m3fn (the K2 conversion:
     megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:53-55, :121-142)."""
@@ -236,7 +245,7 @@ def swiglu_k2(h: torch.Tensor, route_weight: torch.Tensor, clamp: Optional[float
         u = torch.clamp(u, -c, c)
         g = torch.clamp(g, max=c)
     w = route_weight.float().view(-1, 1)
-    return g * (1.0 / (1.0 + torch.exp(-g))) * u * w
+    return g * fdiv(1.0, 1.0 + torch.exp(-g)) * u * w
 
 
 def swiglu_quant_k2(h: torch.Tensor, route_weight: torch.Tensor,
@@ -249,7 +258,7 @@ def swiglu_quant_k2(h: torch.Tensor, route_weight: torch.Tensor,
     y = swiglu_k2(h, route_weight, clamp)
     amax = y.abs().amax(dim=1) if inter > 0 else torch.zeros(rows)
     a = torch.clamp(amax, min=AMAX_FLOOR)
-    inv = (E4M3_MAX / a).view(-1, 1)
+    inv = fdiv(E4M3_MAX, a).view(-1, 1)
     q = e4m3_from_f32(y * inv)
     scale = a / E4M3_MAX
     zero_rows = route_weight.float() == 0.0

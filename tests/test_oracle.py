@@ -228,6 +228,19 @@ def test_gemm_small_integers_exact_and_float64():
     assert O.calc_diff(out, ref) < 1e-12
 
 
+# ------------------------------------------------------------------ fp32 division
+def test_fdiv_is_correctly_rounded():
+    """O.fdiv == the float64 quotient rounded once to float32 (a correctly rounded fp32 divide),
+    on values where torch's reciprocal-then-multiply for scalar/tensor differs."""
+    rng = np.random.default_rng(3)
+    a = (rng.random(200000) * 10 + 1e-4).astype(np.float32)
+    exact = (448.0 / a.astype(np.float64)).astype(np.float32)
+    got = O.fdiv(448.0, torch.from_numpy(a)).numpy()
+    assert np.array_equal(got, exact)
+    recip = (448.0 / torch.from_numpy(a)).numpy()
+    assert not np.array_equal(recip, exact), "torch scalar/tensor path expected to differ"
+
+
 # ------------------------------------------------------------------ SwiGLU + requant
 def test_swiglu_quant_special_rows():
     inter = 8
