@@ -232,7 +232,7 @@ def main() -> int:
 
     roofline = None
     if stage_ms is not None:
-        stage_ms["gemm1"] = stage_ms.pop("gemm1_swiglu_quant")
+        stage_ms["gemm1"] = stage_ms.pop("gemm1_swiglu")
         dom = max(("gemm1", "gemm2"), key=lambda k: stage_ms[k])
         dom_s = stage_ms[dom] * 1e-3
         if bound == "hbm":

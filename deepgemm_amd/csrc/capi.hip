@@ -54,7 +54,6 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->m_indices_offset = take(rows * 4);
   l->act_scale_offset = take(rows * 4);
   l->amax_offset = take(rows * 4);
-  l->done_offset = take(rows * 4);
   l->y_offset = take(rows * static_cast<int64_t>(intermediate) * 4);
   l->act_offset = take(rows * static_cast<int64_t>(intermediate));
   l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
@@ -158,7 +157,6 @@ mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratc
   r.row_weight = at<float>(ws, l.row_weight_offset);
   r.m_indices = at<int32_t>(ws, l.m_indices_offset);
   r.row_amax = at<uint32_t>(ws, l.amax_offset);
-  r.row_done = at<int32_t>(ws, l.done_offset);
   return r;
 }
 
@@ -301,12 +299,16 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   g1.sw.row_weight = at<float>(ws, l.row_weight_offset);
   g1.sw.y = at<float>(ws, l.y_offset);
   g1.sw.amax = at<uint32_t>(ws, l.amax_offset);
-  g1.sw.done = at<int32_t>(ws, l.done_offset);
-  g1.sw.act = at<uint8_t>(ws, l.act_offset);
-  g1.sw.act_scale = at<float>(ws, l.act_scale_offset);
   g1.sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
   g1.sw.clamp = a->activation_clamp;
   if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
+    return MMOE_ERR_HIP;
+
+  if (runs(MMOE_STAGE_REQUANT) &&
+      mmoe::launch_requant(at<float>(ws, l.y_offset), at<uint32_t>(ws, l.amax_offset),
+                           at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
+                           at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, cus,
+                           s) != hipSuccess)
     return MMOE_ERR_HIP;
 
   if (runs(MMOE_STAGE_GEMM2)) {

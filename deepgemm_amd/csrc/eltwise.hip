@@ -14,6 +14,30 @@ namespace {
 constexpr int kEltThreads = 256;
 constexpr int kEltWaves = kEltThreads / kWave;
 
+// ---------------------------------------------------------------- requant
+// One wave per row: a = max(amax, 1e-4); act = e4m3(clip(y * (448/a))); act_scale = a/448.
+// (The K2 requant, megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:341-364, with the
+// row max already reduced by GEMM1's epilogue.)
+__global__ __launch_bounds__(kEltThreads) void requant_kernel(const float* y, const uint32_t* amax,
+                                                              const int32_t* meta, uint8_t* act,
+                                                              float* act_scale, int inter) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int rows = meta[0];
+  const int groups = inter >> 2;
+  for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
+    const float a = fmaxf(__uint_as_float(amax[row]), kAmaxFloor);
+    const float inv = kE4m3Max / a;
+    const float4* yr = reinterpret_cast<const float4*>(y + static_cast<int64_t>(row) * inter);
+    uint32_t* ar = reinterpret_cast<uint32_t*>(act + static_cast<int64_t>(row) * inter);
+    for (int q = lane; q < groups; q += kWave) {
+      const float4 v = yr[q];
+      ar[q] = pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+    }
+    if (lane == 0) act_scale[row] = a / kE4m3Max;
+  }
+}
+
 // ---------------------------------------------------------------- combine
 // One workgroup per token (grid-stride); each thread owns 8-element (16-byte) columns.
 __global__ __launch_bounds__(kEltThreads) void combine_kernel(CombineArgs c) {
@@ -171,6 +195,17 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 }
 
 }  // namespace
+
+hipError_t launch_requant(const float* y, const uint32_t* amax, const int32_t* meta,
+                          uint8_t* act, float* act_scale, int64_t max_rows, int inter,
+                          int num_cus, hipStream_t stream) {
+  if (max_rows <= 0) return hipSuccess;
+  if (inter % 4) return hipErrorInvalidValue;
+  const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 4);
+  hipLaunchKernelGGL(requant_kernel, dim3(grid), dim3(kEltThreads), 0, stream, y, amax, meta, act,
+                     act_scale, inter);
+  return hipGetLastError();
+}
 
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream) {
   if (c.host_tokens <= 0) return hipSuccess;

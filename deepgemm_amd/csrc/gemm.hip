@@ -9,8 +9,10 @@
 //   y = silu(min(h_g, c)) * clamp(h_u, -c, c) * w    (fp32, left to right)
 //   amax[row] = max |y| over the row (atomic max of the float bits: order-free, deterministic)
 // Each output tile holds matching gate and up channels, so SwiGLU is elementwise in registers.
-// The last tile to finish an M-tile (a per-M-tile counter) requantises its rows:
-//   a = max(amax, 1e-4); act = e4m3(clip(y * 448/a)); act_scale = a/448.
+// The per-row requant (a = max(amax, 1e-4); act = e4m3(clip(y * 448/a)); act_scale = a/448)
+// runs as its own small kernel: a cross-workgroup hand-off inside GEMM1 would need an
+// agent-scope release per tile, which on gfx950 writes back the whole (per-XCD, non-coherent)
+// L2 -- measured 4x slower than the kernel boundary.
 // GEMM2 (down, K = I) reads act/act_scale and writes the bf16 partial rows for the combine:
 //   part[r, n] = bf16((sum_k act[r,k] * w2[e,n,k]) * act_scale[r] * w2_sf[e,n]).
 //
@@ -101,31 +103,6 @@ __device__ __forceinline__ float half_wave_max(float v) {
 #pragma unroll
   for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
   return v;
-}
-
-// The last of the `target` tiles of an M-tile requantises its rows [row0, row0+mrows).
-__device__ void finish_mtile(const GemmArgs& g, int row0, int mrows, int target) {
-  __shared__ int s_last;
-  __threadfence();  // release this workgroup's y stores and amax atomics
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(g.sw.done + row0, 1) == target - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();  // acquire every other tile's y and amax
-  const int inter = g.sw.inter;
-  const int groups = inter >> 2;
-  for (int i = threadIdx.x; i < mrows * groups; i += kGemmThreads) {
-    const int r = i / groups;
-    const int q = i - r * groups;
-    const int row = row0 + r;
-    const float a = fmaxf(__uint_as_float(__atomic_load_n(g.sw.amax + row, __ATOMIC_RELAXED)),
-                          kAmaxFloor);
-    const float inv = kE4m3Max / a;
-    const float4 v = reinterpret_cast<const float4*>(g.sw.y + static_cast<int64_t>(row) * inter)[q];
-    reinterpret_cast<uint32_t*>(g.sw.act + static_cast<int64_t>(row) * inter)[q] =
-        pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
-    if (q == 0) g.sw.act_scale[row] = a / kE4m3Max;
-  }
 }
 
 // ------------------------------------------------------------------ STREAM engine
@@ -258,7 +235,6 @@ template <bool kGather, bool kSwiglu>
 __device__ void stream_tile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
   for (int sub = 0; sub * 32 < mrows; ++sub)
     stream_subtile<kGather, kSwiglu>(g, e, row0 + sub * 32, min(32, mrows - sub * 32), nb, smem);
-  if (kSwiglu) finish_mtile(g, row0, mrows, g.n / kStreamBN);
 }
 
 // ------------------------------------------------------------------ TILE engine
@@ -401,7 +377,6 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int nb,
         if (ok && (lane & 31) == 0) atomicMax(g.sw.amax + row, __float_as_uint(m));
       }
     }
-    finish_mtile(g, row0, mrows, g.n / kTileBN);
   }
 }
 

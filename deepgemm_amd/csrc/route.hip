@@ -100,7 +100,6 @@ __device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t ta
     if (a.row_weight != nullptr) a.row_weight[row] = w;
     if (a.m_indices != nullptr) a.m_indices[row] = e;
     if (a.row_amax != nullptr) a.row_amax[row] = 0u;
-    if (a.row_done != nullptr) a.row_done[row] = 0;
   }
 }
 

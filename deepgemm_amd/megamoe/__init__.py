@@ -513,9 +513,9 @@ def _launch_layer(y, l1_weights, l2_weights, stats, sym_buffer, activation_clamp
 class LayerCall:
     """A prepared layer call whose stages can be launched one at a time (profiling, stage
     parity). ``run(first, last)`` launches stages [first, last] on the current stream:
-    0 route, 1 GEMM1 with the fused SwiGLU + requant, 2 GEMM2, 3 combine."""
+    0 route, 1 GEMM1 with the fused SwiGLU x weight, 2 requant, 3 GEMM2, 4 combine."""
 
-    STAGES = ("route", "gemm1_swiglu_quant", "gemm2", "combine")
+    STAGES = ("route", "gemm1_swiglu", "requant", "gemm2", "combine")
 
     def __init__(self, y, l1_weights, l2_weights, sym_buffer, activation_clamp=None,
                  staged: Optional[bool] = None, stats=None):
@@ -529,7 +529,7 @@ class LayerCall:
         self.args = _forward_args(y, l1_weights, l2_weights, stats, sym_buffer,
                                   activation_clamp, schedule)
 
-    def run(self, first: int = 0, last: int = 3) -> None:
+    def run(self, first: int = 0, last: int = 4) -> None:
         _capi.check(_capi.load().mmoe_forward_stages(ctypes.byref(self.args), first, last,
                                                      _stream_handle()), "fp8_mega_moe")
 

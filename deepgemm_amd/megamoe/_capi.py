@@ -48,7 +48,6 @@ class ScratchLayout(ctypes.Structure):
         ("m_indices_offset", c_i64),
         ("act_scale_offset", c_i64),
         ("amax_offset", c_i64),
-        ("done_offset", c_i64),
         ("y_offset", c_i64),
         ("act_offset", c_i64),
         ("part_offset", c_i64),

@@ -84,7 +84,6 @@ typedef struct mmoe_scratch_layout {
   int64_t m_indices_offset;    /* int32 [rows] local expert of each routed row */
   int64_t act_scale_offset;    /* f32   [rows] per-row FP8 scale of the SwiGLU output */
   int64_t amax_offset;         /* u32   [rows] float bits of max |y| per row */
-  int64_t done_offset;         /* int32 [rows] finished-tile counters of the GEMM1 M-tiles */
   int64_t y_offset;            /* f32   [rows, I]  SwiGLU x weight output of GEMM1 */
   int64_t act_offset;          /* e4m3  [rows, I]  requantised SwiGLU output */
   int64_t part_offset;         /* bf16  [rows, H]  per-row GEMM2 output (combine partials) */
@@ -145,18 +144,18 @@ const char* mmoe_status_string(int status);
 
 /* The layer: fp8_mega_moe / fp8_mega_moe_with_graph_tokens,
  * csrc/apis/mega_dcu.hpp:338-518 -> csrc/kernels/mega_moe_fused_hip.cu:72-121 and the staged
- * path megamoe/large_opt.py:367-508. Routing -> GEMM1 with fused SwiGLU+requant -> GEMM2 ->
- * combine. */
+ * path megamoe/large_opt.py:367-508. Routing -> GEMM1 with fused SwiGLU -> requant -> GEMM2
+ * -> combine. */
 int mmoe_forward(const mmoe_forward_args* args, void* stream);
 
 /* Stages of mmoe_forward, in order; each reads what the earlier ones left in route_scratch. */
 #define MMOE_STAGE_ROUTE 0   /* counts, offsets, output_index, per-row tables, stats */
-#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I], amax, then
-                                the per-row requant -> act e4m3 [R, I] + act_scale [R] */
-#define MMOE_STAGE_GEMM2 2   /* part bf16 [R, H] */
-#define MMOE_STAGE_COMBINE 3 /* y */
+#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I] + row max |y| */
+#define MMOE_STAGE_REQUANT 2 /* act e4m3 [R, I] + act_scale [R] */
+#define MMOE_STAGE_GEMM2 3   /* part bf16 [R, H] */
+#define MMOE_STAGE_COMBINE 4 /* y */
 
-/* Runs stages [first_stage, last_stage] of mmoe_forward (mmoe_forward = stages 0..3). Lets a
+/* Runs stages [first_stage, last_stage] of mmoe_forward (mmoe_forward = stages 0..4). Lets a
  * profiler bracket each kernel with events and lets tests check each stage on its own. The
  * reference runs the same stages as K1/K2/K3 (megamoe/large_opt.py:367-508). */
 int mmoe_forward_stages(const mmoe_forward_args* args, int first_stage, int last_stage,

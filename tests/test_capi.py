@@ -95,7 +95,7 @@ def test_layouts():
     assert lay.row_capacity >= 384 * 6
     offs = [lay.counts_offset, lay.offsets_offset, lay.meta_offset, lay.chunk_counts_offset,
             lay.output_index_offset, lay.row_token_offset, lay.row_weight_offset,
-            lay.m_indices_offset, lay.act_scale_offset, lay.amax_offset, lay.done_offset,
+            lay.m_indices_offset, lay.act_scale_offset, lay.amax_offset,
             lay.y_offset, lay.act_offset,
             lay.part_offset]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
