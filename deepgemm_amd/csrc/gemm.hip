@@ -19,14 +19,14 @@
 // B is the Marlin nt_kpack2 weight (deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:50-66):
 // per 16-row tile, each 16-byte k-block of the 16 rows is 256 contiguous bytes.
 //
-// One persistent kernel per GEMM, two tile engines chosen per expert on the device from its
-// routed row count:
-//  * STREAM engine (<= 64 rows: decode, HBM-bound on the weights). Tile = (expert, 64 output
-//    columns, all rows). The four waves split K; each wave loads its MFMA operands straight from
-//    global memory into registers (Marlin gives each lane 16 contiguous k-bytes of one weight
-//    row; 16 lanes read 256 contiguous bytes) through a straight-line register ring 4 steps
-//    deep, with no LDS and no barrier in the K loop, one 32-row subtile at a time. The
-//    K-partials are summed through LDS in a fixed order.
+// Two persistent kernels per GEMM (two tile engines); each expert's engine is chosen on the
+// device from its routed row count and each kernel skips the other engine's experts:
+//  * STREAM engine (<= 64 rows: decode, HBM-bound on the weights). One wave per tile =
+//    (expert, 64 output columns, all <= 64 rows) over the full K; the wave loads its MFMA
+//    operands straight from global memory into registers (Marlin gives each lane 16 contiguous
+//    k-bytes of one weight row; 16 lanes read 256 contiguous bytes) through a straight-line
+//    register ring 4 steps deep, with no LDS and no barrier. With ~2 waves per SIMD there are
+//    about as many resident waves as decode tiles, so a wave streams one long tile.
 //  * TILE engine (more rows: prefill, MFMA-bound). 128x128 output tiles, BK = 128, A and B
 //    staged through double-buffered LDS in 16-row x 16-byte blocks (block (rb, kb) at
 //    (rb*BK/16 + kb)*256); a 32x32x64 MFMA operand of lane l (row l%32, k-half l/32) is two
@@ -40,12 +40,11 @@ namespace mmoe {
 
 namespace {
 
-constexpr int kGemmThreads = 256;
-constexpr int kGemmWaves = kGemmThreads / kWave;
+constexpr int kGemmThreads = 256;  // TILE engine workgroup
 constexpr int kMaxGemmExperts = 256;
 constexpr int kStreamMaxRows = 64;  // experts up to this many rows use the STREAM engine
 constexpr int kStreamBN = 64;
-constexpr int kStreamDepth = 4;     // register ring depth: 64-k steps in flight per wave
+constexpr int kStreamDepth = 4;     // register ring depth (64-k steps in flight), one subtile
 constexpr int kTileBM = 128, kTileBN = 128, kTileBK = 128;
 constexpr int kTileWM = 2, kTileWN = 2;
 constexpr int kSmemBytes = 65536;
@@ -106,52 +105,64 @@ __device__ __forceinline__ float half_wave_max(float v) {
 }
 
 // ------------------------------------------------------------------ STREAM engine
-// One 32-row subtile of a STREAM tile: the full K pass, the K-partial reduction and the epilogue.
-template <bool kGather, bool kSwiglu>
-__device__ void stream_subtile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
-  constexpr int kDepth = kStreamDepth;
+// One wave computes a whole tile: (expert, 64 output columns, MT 32-row subtiles) over the full
+// K, so there is no cross-wave reduction and no barrier. Its MFMA operands come straight from
+// global memory into a register ring kStreamDepth steps deep: every load is unconditional and
+// the scheduling barriers keep the issue order slot by slot, so the compiler's wait for a slot
+// leaves the younger slots in flight. The k order of the accumulation is the same as the TILE
+// engine's (sequential 64-k steps), so both engines produce the same bits.
+template <bool kGather, bool kSwiglu, int MT>
+__device__ void stream_wave_tile(const GemmArgs& g, int e, int row0, int mrows, int nb) {
+  constexpr int kDepth = MT == 1 ? kStreamDepth : kStreamDepth - 1;
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
-  const int ksteps = g.k / 64;
-  const int s_begin = wave * ksteps / kGemmWaves;
-  const int nsteps = (wave + 1) * ksteps / kGemmWaves - s_begin;
+  const int nsteps = g.k / 64;
 
-  const int r_lane = lane & 31;
-  const uint8_t* ap = a_row_ptr<kGather>(g, row0 + (r_lane < mrows ? r_lane : 0)) +
-                      (lane >> 5) * 32 + s_begin * 64;
+  const uint8_t* ap[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r = mt * 32 + (lane & 31);
+    ap[mt] = a_row_ptr<kGather>(g, row0 + (r < mrows ? r : 0)) + (lane >> 5) * 32;
+  }
   const uint8_t* bp[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const int n = weight_row<kSwiglu>(g, nb, kStreamBN, ct * 32 + (lane & 31));
     bp[ct] = g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) +
-             (n & 15) * 16 + (lane >> 5) * 512 + static_cast<int64_t>(s_begin) * 1024;
+             (n & 15) * 16 + (lane >> 5) * 512;
   }
 
-  int4 ar[kDepth][2];
+  int4 ar[kDepth][MT][2];
   int4 br[kDepth][2][2];
   auto issue = [&](int slot, int s) {
-    ar[slot][0] = ld16(ap + s * 64);
-    ar[slot][1] = ld16(ap + s * 64 + 16);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       br[slot][ct][0] = ld16(bp[ct] + static_cast<int64_t>(s) * 1024);
       br[slot][ct][1] = ld16(bp[ct] + static_cast<int64_t>(s) * 1024 + 256);
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      ar[slot][mt][0] = ld16(ap[mt] + s * 64);
+      ar[slot][mt][1] = ld16(ap[mt] + s * 64 + 16);
+    }
   };
-  v16f acc[2];
+  v16f acc[MT][2];
 #pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[ct][v] = 0.0f;
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mt][ct][v] = 0.0f;
   auto compute = [&](int slot) {
-    const v8i a = make_v8i(ar[slot][0], ar[slot][1]);
-    acc[0] = mfma_fp8(a, make_v8i(br[slot][0][0], br[slot][0][1]), acc[0]);
-    acc[1] = mfma_fp8(a, make_v8i(br[slot][1][0], br[slot][1][1]), acc[1]);
+    const v8i b0 = make_v8i(br[slot][0][0], br[slot][0][1]);
+    const v8i b1 = make_v8i(br[slot][1][0], br[slot][1][1]);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const v8i a = make_v8i(ar[slot][mt][0], ar[slot][mt][1]);
+      acc[mt][0] = mfma_fp8(a, b0, acc[mt][0]);
+      acc[mt][1] = mfma_fp8(a, b1, acc[mt][1]);
+    }
   };
   if (nsteps >= kDepth && nsteps % kDepth == 0) {
-    // Straight-line ring: every load is unconditional and the scheduling barriers keep the
-    // issue order slot by slot, so a slot's loads are the oldest in flight when it is consumed
-    // (the compiler's wait = vmcnt of the younger slots).
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) {
       issue(d, d);
@@ -168,73 +179,50 @@ __device__ void stream_subtile(const GemmArgs& g, int e, int row0, int mrows, in
 #pragma unroll
     for (int d = 0; d < kDepth; ++d) compute(d);
   } else {
-    // short or uneven K slices (small shapes): one step at a time
-    for (int s = 0; s < nsteps; ++s) {
+    for (int s = 0; s < nsteps; ++s) {  // short K (small shapes): one step at a time
       issue(0, s);
       compute(0);
     }
   }
 
-  // fixed-order reduction of the four K partials: red[wave][ct][v][lane]
-  float* red = reinterpret_cast<float*>(smem);
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) red[((wave * 2 + ct) * 16 + v) * kWave + lane] = acc[ct][v];
-  __syncthreads();
-  auto partial_sum = [&](int ct, int v) {
-    float s = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kGemmWaves; ++w) s += red[((w * 2 + ct) * 16 + v) * kWave + lane];
-    return s;
-  };
-  // wave w finishes registers v in [4w, 4w+4) (rows 8*w + 4*(lane/32) + 0..3) of both columns
   if (!kSwiglu) {
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       const int col = nb * kStreamBN + ct * 32 + (lane & 31);
       const float bs = g.b_scale[static_cast<int64_t>(e) * g.n + col];
 #pragma unroll
-      for (int vv = 0; vv < 4; ++vv) {
-        const int v = wave * 4 + vv;
-        const float s = partial_sum(ct, v);
-        const int r = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (r < mrows) {
-          const int row = row0 + r;
-          g.c[static_cast<int64_t>(row) * g.n + col] = f32_to_bf16(s * row_scale<kGather>(g, row) * bs);
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = mt * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+          if (r < mrows) {
+            const int row = row0 + r;
+            g.c[static_cast<int64_t>(row) * g.n + col] =
+                f32_to_bf16(acc[mt][ct][v] * row_scale<kGather>(g, row) * bs);
+          }
         }
-      }
     }
   } else {
     const int chan = nb * (kStreamBN / 2) + (lane & 31);
     const float wsg = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
     const float wsu = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
 #pragma unroll
-    for (int vv = 0; vv < 4; ++vv) {
-      const int v = wave * 4 + vv;
-      const float ga = partial_sum(0, v);
-      const float ua = partial_sum(1, v);
-      const int r = (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      float yv = 0.0f;
-      const bool ok = r < mrows;
-      const int row = row0 + (ok ? r : 0);
-      if (ok) {
-        yv = swiglu_value(g, ga, ua, row_scale<kGather>(g, row), wsg, wsu, g.sw.row_weight[row]);
-        g.sw.y[static_cast<int64_t>(row) * g.sw.inter + chan] = yv;
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = mt * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        const bool ok = r < mrows;
+        const int row = row0 + (ok ? r : 0);
+        float yv = 0.0f;
+        if (ok) {
+          yv = swiglu_value(g, acc[mt][0][v], acc[mt][1][v], row_scale<kGather>(g, row), wsg, wsu,
+                            g.sw.row_weight[row]);
+          g.sw.y[static_cast<int64_t>(row) * g.sw.inter + chan] = yv;
+        }
+        const float m = half_wave_max(fabsf(yv));
+        if (ok && (lane & 31) == 0) atomicMax(g.sw.amax + row, __float_as_uint(m));
       }
-      const float m = half_wave_max(fabsf(yv));
-      if (ok && (lane & 31) == 0) atomicMax(g.sw.amax + row, __float_as_uint(m));
-    }
   }
-  __syncthreads();  // the reduction buffer is reused by the next subtile / tile
-}
-
-// A STREAM tile: (expert, 64 columns, <= 64 rows) as one or two 32-row subtiles; the second
-// subtile re-reads the same weight slice, which the first left in L2.
-template <bool kGather, bool kSwiglu>
-__device__ void stream_tile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
-  for (int sub = 0; sub * 32 < mrows; ++sub)
-    stream_subtile<kGather, kSwiglu>(g, e, row0 + sub * 32, min(32, mrows - sub * 32), nb, smem);
 }
 
 // ------------------------------------------------------------------ TILE engine
@@ -380,12 +368,10 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int nb,
   }
 }
 
-// ------------------------------------------------------------------ persistent dispatcher
-template <bool kGather, bool kSwiglu>
-__global__ __launch_bounds__(kGemmThreads, 2) void grouped_gemm_kernel(GemmArgs g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  __shared__ int s_prefix[kMaxGemmExperts + 1];
-  __shared__ unsigned char s_tile_engine[kMaxGemmExperts];
+// ------------------------------------------------------------------ persistent dispatchers
+// Wave 0 of the workgroup fills s_prefix[0..E] with the exclusive prefix of the tiles of the
+// experts this kernel owns (`tile_kernel`: experts on the TILE engine, else STREAM).
+__device__ void enumerate_tiles(const GemmArgs& g, bool tile_kernel, int* s_prefix) {
   const int E = g.num_experts;
   const int lane = lane_id();
   if (threadIdx.x < kWave) {
@@ -397,9 +383,9 @@ __global__ __launch_bounds__(kGemmThreads, 2) void grouped_gemm_kernel(GemmArgs 
         const int cnt = g.counts[e];
         const bool tile = g.engine == GemmEngine::kTile ||
                           (g.engine == GemmEngine::kAuto && cnt > kStreamMaxRows);
-        s_tile_engine[e] = tile ? 1 : 0;
-        tiles = tile ? (cnt + kTileBM - 1) / kTileBM * (g.n / kTileBN)
-                     : (cnt + kStreamMaxRows - 1) / kStreamMaxRows * (g.n / kStreamBN);
+        if (tile == tile_kernel)
+          tiles = tile ? (cnt + kTileBM - 1) / kTileBM * (g.n / kTileBN)
+                       : (cnt + kStreamMaxRows - 1) / kStreamMaxRows * (g.n / kStreamBN);
       }
       int inc = tiles;
 #pragma unroll
@@ -412,32 +398,82 @@ __global__ __launch_bounds__(kGemmThreads, 2) void grouped_gemm_kernel(GemmArgs 
     }
     if (lane == 0) s_prefix[E] = carry;
   }
+}
+
+__device__ __forceinline__ int expert_of_tile(const int* s_prefix, int E, int t) {
+  int lo = 0, hi = E;  // last e with s_prefix[e] <= t
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (s_prefix[mid] <= t) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+template <bool kGather, bool kSwiglu>
+__global__ __launch_bounds__(kWave, 2) void stream_gemm_kernel(GemmArgs g) {
+  __shared__ int s_prefix[kMaxGemmExperts + 1];
+  enumerate_tiles(g, false, s_prefix);
   __syncthreads();
+  const int E = g.num_experts;
   const int total = s_prefix[E];
+  const int nt = g.n / kStreamBN;
   for (int t = blockIdx.x; t < total; t += gridDim.x) {
-    int lo = 0, hi = E;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_prefix[mid] <= t) lo = mid; else hi = mid;
-    }
-    const int e = lo;
+    const int e = expert_of_tile(s_prefix, E, t);
     const int local = t - s_prefix[e];
-    const int cnt = g.counts[e];
-    if (s_tile_engine[e]) {
-      const int nt = g.n / kTileBN;
-      const int mt = local / nt;
-      const int nb = local - mt * nt;
-      tile_tile<kGather, kSwiglu>(g, e, g.offsets[e] + mt * kTileBM,
-                                  min(kTileBM, cnt - mt * kTileBM), nb, smem);
-    } else {
-      const int nt = g.n / kStreamBN;
-      const int mt = local / nt;
-      const int nb = local - mt * nt;
-      stream_tile<kGather, kSwiglu>(g, e, g.offsets[e] + mt * kStreamMaxRows,
-                                    min(kStreamMaxRows, cnt - mt * kStreamMaxRows), nb, smem);
-    }
+    const int mt = local / nt;
+    const int nb = local - mt * nt;
+    const int row0 = g.offsets[e] + mt * kStreamMaxRows;
+    const int mrows = min(kStreamMaxRows, g.counts[e] - mt * kStreamMaxRows);
+    if (mrows > 32)
+      stream_wave_tile<kGather, kSwiglu, 2>(g, e, row0, mrows, nb);
+    else
+      stream_wave_tile<kGather, kSwiglu, 1>(g, e, row0, mrows, nb);
+  }
+}
+
+template <bool kGather, bool kSwiglu>
+__global__ __launch_bounds__(kGemmThreads, 2) void tile_gemm_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_prefix[kMaxGemmExperts + 1];
+  enumerate_tiles(g, true, s_prefix);
+  __syncthreads();
+  const int E = g.num_experts;
+  const int total = s_prefix[E];
+  const int nt = g.n / kTileBN;
+  for (int t = blockIdx.x; t < total; t += gridDim.x) {
+    const int e = expert_of_tile(s_prefix, E, t);
+    const int local = t - s_prefix[e];
+    const int mt = local / nt;
+    const int nb = local - mt * nt;
+    tile_tile<kGather, kSwiglu>(g, e, g.offsets[e] + mt * kTileBM,
+                                min(kTileBM, g.counts[e] - mt * kTileBM), nb, smem);
     __syncthreads();
   }
+}
+
+template <bool kGather, bool kSwiglu>
+hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
+  if (g.engine != GemmEngine::kTile) {
+    const int64_t tiles =
+        (static_cast<int64_t>(max_rows) / kStreamMaxRows + g.num_experts) * (g.n / kStreamBN);
+    int64_t grid = static_cast<int64_t>(num_cus) * 8;  // 2 waves per SIMD
+    if (grid > tiles) grid = tiles;
+    hipLaunchKernelGGL((stream_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
+                       dim3(kWave), 0, stream, g);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  if (g.engine != GemmEngine::kStream) {
+    const int64_t tiles =
+        (static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * (g.n / kTileBN);
+    int64_t grid = static_cast<int64_t>(num_cus) * 2;
+    if (grid > tiles) grid = tiles;
+    hipLaunchKernelGGL((tile_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
+                       dim3(kGemmThreads), kSmemBytes, stream, g);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
 }
 
 }  // namespace
@@ -449,22 +485,12 @@ bool gemm_shape_supported(int n, int k) {
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
   if (max_rows <= 0) return hipSuccess;
   if (g.num_experts > kMaxGemmExperts) return hipErrorInvalidValue;
-  // upper bound of the tiles of either engine, for the persistent grid size
-  const int64_t stream_tiles =
-      (static_cast<int64_t>(max_rows) / kStreamMaxRows + g.num_experts) * (g.n / kStreamBN);
-  int64_t grid = static_cast<int64_t>(num_cus) * 2;
-  if (grid > stream_tiles) grid = stream_tiles;
-  if (grid < 1) grid = 1;
   if (g.sw.enabled) {
     if (g.row_token == nullptr || g.n != 2 * g.sw.inter) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((grouped_gemm_kernel<true, true>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kGemmThreads), kSmemBytes, stream, g);
-  } else {
-    if (g.row_token != nullptr) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((grouped_gemm_kernel<false, false>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kGemmThreads), kSmemBytes, stream, g);
+    return launch_engines<true, true>(g, max_rows, num_cus, stream);
   }
-  return hipGetLastError();
+  if (g.row_token != nullptr) return hipErrorInvalidValue;
+  return launch_engines<false, false>(g, max_rows, num_cus, stream);
 }
 
 }  // namespace mmoe
