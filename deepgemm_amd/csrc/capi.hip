@@ -156,7 +156,6 @@ mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratc
   r.row_token = at<int32_t>(ws, l.row_token_offset);
   r.row_weight = at<float>(ws, l.row_weight_offset);
   r.m_indices = at<int32_t>(ws, l.m_indices_offset);
-  r.row_amax = at<uint32_t>(ws, l.amax_offset);
   return r;
 }
 
@@ -298,14 +297,13 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   g1.sw.inter = a->intermediate;
   g1.sw.row_weight = at<float>(ws, l.row_weight_offset);
   g1.sw.y = at<float>(ws, l.y_offset);
-  g1.sw.amax = at<uint32_t>(ws, l.amax_offset);
   g1.sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
   g1.sw.clamp = a->activation_clamp;
   if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
   if (runs(MMOE_STAGE_REQUANT) &&
-      mmoe::launch_requant(at<float>(ws, l.y_offset), at<uint32_t>(ws, l.amax_offset),
+      mmoe::launch_requant(at<float>(ws, l.y_offset), at<float>(ws, l.amax_offset),
                            at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
                            at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, cus,
                            s) != hipSuccess)

@@ -15,10 +15,17 @@ constexpr int kEltThreads = 256;
 constexpr int kEltWaves = kEltThreads / kWave;
 
 // ---------------------------------------------------------------- requant
-// One wave per row: a = max(amax, 1e-4); act = e4m3(clip(y * (448/a))); act_scale = a/448.
-// (The K2 requant, megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:341-364, with the
-// row max already reduced by GEMM1's epilogue.)
-__global__ __launch_bounds__(kEltThreads) void requant_kernel(const float* y, const uint32_t* amax,
+// One wave per row: amax = max |y|; a = max(amax, 1e-4); act = e4m3(clip(y * (448/a)));
+// act_scale = a/448 (the K2 requant, megamoe/dcu_megamoe_large_opt/K2_fused/
+// k2_fused_ext.cu:341-364). A row of up to kRequantGroups*4*64 channels stays in registers
+// between the reduction and the quantization; a longer one is read twice.
+constexpr int kRequantGroups = 8;  // float4 groups per lane held in registers
+
+__device__ __forceinline__ float abs_max4(float m, const float4& v) {
+  return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+__global__ __launch_bounds__(kEltThreads) void requant_kernel(const float* y, float* amax,
                                                               const int32_t* meta, uint8_t* act,
                                                               float* act_scale, int inter) {
   const int lane = lane_id();
@@ -26,15 +33,37 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(const float* y, co
   const int rows = meta[0];
   const int groups = inter >> 2;
   for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
-    const float a = fmaxf(__uint_as_float(amax[row]), kAmaxFloor);
-    const float inv = kE4m3Max / a;
     const float4* yr = reinterpret_cast<const float4*>(y + static_cast<int64_t>(row) * inter);
     uint32_t* ar = reinterpret_cast<uint32_t*>(act + static_cast<int64_t>(row) * inter);
-    for (int q = lane; q < groups; q += kWave) {
-      const float4 v = yr[q];
-      ar[q] = pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+    float m = 0.0f;
+    if (groups <= kRequantGroups * kWave) {
+      float4 v[kRequantGroups];
+#pragma unroll
+      for (int i = 0; i < kRequantGroups; ++i) {
+        const int q = lane + i * kWave;
+        v[i] = q < groups ? yr[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        m = abs_max4(m, v[i]);
+      }
+      m = wave_max(m);
+      const float inv = kE4m3Max / fmaxf(m, kAmaxFloor);
+#pragma unroll
+      for (int i = 0; i < kRequantGroups; ++i) {
+        const int q = lane + i * kWave;
+        if (q < groups) ar[q] = pack_e4m3x4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+      }
+    } else {
+      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, yr[q]);
+      m = wave_max(m);
+      const float inv = kE4m3Max / fmaxf(m, kAmaxFloor);
+      for (int q = lane; q < groups; q += kWave) {
+        const float4 v = yr[q];
+        ar[q] = pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+      }
     }
-    if (lane == 0) act_scale[row] = a / kE4m3Max;
+    if (lane == 0) {
+      amax[row] = m;
+      act_scale[row] = fmaxf(m, kAmaxFloor) / kE4m3Max;
+    }
   }
 }
 
@@ -196,7 +225,7 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 
 }  // namespace
 
-hipError_t launch_requant(const float* y, const uint32_t* amax, const int32_t* meta,
+hipError_t launch_requant(const float* y, float* amax, const int32_t* meta,
                           uint8_t* act, float* act_scale, int64_t max_rows, int inter,
                           int num_cus, hipStream_t stream) {
   if (max_rows <= 0) return hipSuccess;

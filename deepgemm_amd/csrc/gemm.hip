@@ -7,32 +7,38 @@
 // (megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:254-377) into its epilogue:
 //   h = bf16(acc * x_sf[token] * w1_sf[e, n])       for the gate and the up column of a channel
 //   y = silu(min(h_g, c)) * clamp(h_u, -c, c) * w    (fp32, left to right)
-//   amax[row] = max |y| over the row (atomic max of the float bits: order-free, deterministic)
 // Each output tile holds matching gate and up channels, so SwiGLU is elementwise in registers.
-// The per-row requant (a = max(amax, 1e-4); act = e4m3(clip(y * 448/a)); act_scale = a/448)
-// runs as its own small kernel: a cross-workgroup hand-off inside GEMM1 would need an
-// agent-scope release per tile, which on gfx950 writes back the whole (per-XCD, non-coherent)
-// L2 -- measured 4x slower than the kernel boundary.
+// The per-row requant (amax = max |y|; a = max(amax, 1e-4); act = e4m3(clip(y * 448/a));
+// act_scale = a/448) needs the whole row and runs as its own small kernel: a cross-workgroup
+// hand-off inside GEMM1 would need an agent-scope release per tile, which on gfx950 writes back
+// the whole (per-XCD, non-coherent) L2 -- measured 4x slower than the kernel boundary.
 // GEMM2 (down, K = I) reads act/act_scale and writes the bf16 partial rows for the combine:
 //   part[r, n] = bf16((sum_k act[r,k] * w2[e,n,k]) * act_scale[r] * w2_sf[e,n]).
 //
 // B is the Marlin nt_kpack2 weight (deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:50-66):
 // per 16-row tile, each 16-byte k-block of the 16 rows is 256 contiguous bytes.
 //
-// Two persistent kernels per GEMM (two tile engines); each expert's engine is chosen on the
-// device from its routed row count and each kernel skips the other engine's experts:
-//  * STREAM engine (<= 64 rows: decode, HBM-bound on the weights). One wave per tile =
-//    (expert, 64 output columns, all <= 64 rows) over the full K; the wave loads its MFMA
-//    operands straight from global memory into registers (Marlin gives each lane 16 contiguous
-//    k-bytes of one weight row; 16 lanes read 256 contiguous bytes) through a straight-line
-//    register ring 4 steps deep, with no LDS and no barrier. With ~2 waves per SIMD there are
-//    about as many resident waves as decode tiles, so a wave streams one long tile.
-//  * TILE engine (more rows: prefill, MFMA-bound). 128x128 output tiles, BK = 128, A and B
-//    staged through double-buffered LDS in 16-row x 16-byte blocks (block (rb, kb) at
-//    (rb*BK/16 + kb)*256); a 32x32x64 MFMA operand of lane l (row l%32, k-half l/32) is two
-//    16-byte reads of consecutive blocks, 16 lanes reading 256 contiguous bytes (conflict-free).
+// One persistent kernel per GEMM, one 8-wave workgroup per CU, runs two tile engines; each
+// expert's engine is chosen on the device from its routed row count:
+//  * STREAM engine (<= 64 rows: decode, HBM-bound on the weights). A workgroup tile is (expert,
+//    512 output columns, <= 64 rows) over the full K; wave w owns columns [64w, 64w + 64) and
+//    streams its weight columns from global memory into a register ring 4 steps deep (Marlin
+//    gives each lane 16 contiguous k-bytes of one weight row; 16 lanes read 256 contiguous
+//    bytes), with no barrier: B never touches LDS. The A rows, the same for the 8 waves, go to
+//    LDS once per workgroup in k-chunks of 64 KB loaded as whole 128-byte lines, double
+//    buffered: chunk c+1 is in flight while chunk c is used, and one barrier per chunk (1-4 per
+//    tile) hands the buffers over. Loading A per wave in MFMA operand order (32 lines per
+//    instruction, re-read by every wave) made the A reads, not the weights, set the pace.
+//  * TILE engine (more rows: prefill, MFMA-bound). Each 4-wave half of the workgroup computes
+//    a 128x128 output tile, BK = 128, A and B staged through double-buffered LDS in 16-row x
+//    16-byte blocks (block (rb, kb) at (rb*BK/16 + kb)*256); a 32x32x64 MFMA operand of lane l
+//    (row l%32, k-half l/32) is two 16-byte reads of consecutive blocks, 16 lanes reading 256
+//    contiguous bytes (conflict-free).
 // In both engines lane l supplies k-bytes [32*(l/32), 32*(l/32)+32) of each 64-k MFMA step for
-// A and B alike; any such bijection gives the same dot product.
+// A and B alike; any such bijection gives the same dot product, and both engines accumulate the
+// 64-k steps in the same order, so they produce the same bits.
+#include <algorithm>
+
 #include "common.cuh"
 #include "kernels.h"
 
@@ -40,14 +46,21 @@ namespace mmoe {
 
 namespace {
 
-constexpr int kGemmThreads = 256;  // TILE engine workgroup
+constexpr int kGemmThreads = 512;  // 8 waves, one workgroup per CU
+constexpr int kGemmWaves = kGemmThreads / kWave;
 constexpr int kMaxGemmExperts = 256;
-constexpr int kStreamMaxRows = 64;  // experts up to this many rows use the STREAM engine
-constexpr int kStreamBN = 64;
-constexpr int kStreamDepth = 4;     // register ring depth (64-k steps in flight), one subtile
+// STREAM engine
+constexpr int kStreamUnit = 64;     // output columns per wave
+constexpr int kStreamRows = 64;     // rows per workgroup tile (experts up to this many use it)
+constexpr int kStreamDepth = 4;     // 64-k weight steps in flight per wave
+constexpr int kAChunk = 65536;      // bytes of one A chunk buffer (32*MT rows x 2048/MT k)
+constexpr int kALoads = kAChunk / 1024 / kGemmWaves;  // 16-byte A loads per lane per chunk
+// TILE engine (per 4-wave half)
+constexpr int kTileThreads = 256;
 constexpr int kTileBM = 128, kTileBN = 128, kTileBK = 128;
 constexpr int kTileWM = 2, kTileWN = 2;
-constexpr int kSmemBytes = 65536;
+constexpr int kTileSmem = 65536;
+constexpr int kSmemBytes = 2 * kAChunk;  // == 2 * kTileSmem
 
 __device__ __forceinline__ v8i make_v8i(const int4& lo, const int4& hi) {
   v8i r;
@@ -97,52 +110,147 @@ __device__ __forceinline__ float swiglu_value(const GemmArgs& g, float gacc, flo
   return gh * (1.0f / (1.0f + expf(-gh))) * uh * route_w;
 }
 
-// max over the 32 lanes of each half-wave (the 32 channels of one output row)
-__device__ __forceinline__ float half_wave_max(float v) {
+// Thread index for an engine body, opaque to the optimizer: values derived from it are computed
+// inside the body instead of being hoisted out of the persistent item loop, where the
+// invariants of every engine variant would stay live at once and crowd out the ring.
+__device__ __forceinline__ int opaque_tid() {
+  int t = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// ------------------------------------------------------------------ epilogue
+// Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
+// the tile (mrows <= 64), 64-column unit `unit` of the output (SwiGLU: 32 channels). Lane t
+// first fetches row row0 + t's A scale and route weight, and the values reach the lanes that
+// need them by shuffles, so the whole epilogue waits for two memory round trips instead of a
+// dependent chain per row.
+template <bool kGather, bool kSwiglu, int MT>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[MT][2], int e,
+                                           int row0, int mrows, int unit) {
+  const int lane = opaque_tid() & (kWave - 1);
+  const int rl = lane & 31, hk = lane >> 5;
+  float m_xs = 0.0f, m_rw = 0.0f;
+  if (lane < mrows) {
+    m_xs = row_scale<kGather>(g, row0 + lane);
+    if (kSwiglu) m_rw = g.sw.row_weight[row0 + lane];
+  }
+  if (!kSwiglu) {
+    float bs[2];
 #pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
+    for (int ct = 0; ct < 2; ++ct) bs[ct] = g.b_scale[static_cast<int64_t>(e) * g.n + unit * 64 + ct * 32 + rl];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
+        const float xs = __shfl(m_xs, r, kWave);
+        if (r < mrows) {
+          uint16_t* crow = g.c + static_cast<int64_t>(row0 + r) * g.n + unit * 64 + rl;
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) crow[ct * 32] = f32_to_bf16(acc[mt][ct][v] * xs * bs[ct]);
+        }
+      }
+  } else {
+    const int chan = unit * 32 + rl;
+    const float wsg = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
+    const float wsu = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
+        const float xs = __shfl(m_xs, r, kWave);
+        const float rw = __shfl(m_rw, r, kWave);
+        if (r < mrows)
+          g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + chan] =
+              swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs, wsg, wsu, rw);
+      }
+  }
 }
 
 // ------------------------------------------------------------------ STREAM engine
-// One wave computes a whole tile: (expert, 64 output columns, MT 32-row subtiles) over the full
-// K, so there is no cross-wave reduction and no barrier. Its MFMA operands come straight from
-// global memory into a register ring kStreamDepth steps deep: every load is unconditional and
-// the scheduling barriers keep the issue order slot by slot, so the compiler's wait for a slot
-// leaves the younger slots in flight. The k order of the accumulation is the same as the TILE
-// engine's (sequential 64-k steps), so both engines produce the same bits.
-template <bool kGather, bool kSwiglu, int MT>
-__device__ void stream_wave_tile(const GemmArgs& g, int e, int row0, int mrows, int nb) {
-  constexpr int kDepth = MT == 1 ? kStreamDepth : kStreamDepth - 1;
-  const int lane = lane_id();
-  const int nsteps = g.k / 64;
+// Workgroup barrier for the LDS A chunks: this wave's LDS writes are complete, then s_barrier.
+// It waits on no global load, so the weight loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
-  const uint8_t* ap[MT];
+// 16-byte piece p of LDS A row r sits at piece (p & ~7) | ((p ^ r) & 7): 8 lanes reading the
+// same k of 8 consecutive rows hit 8 distinct 16-byte bank groups.
+__device__ __forceinline__ int swizzle_piece(int p, int r) { return (p & ~7) | ((p ^ r) & 7); }
+
+// One workgroup tile (expert e, 512-column block nb, rows [row0, row0 + mrows), mrows <= 32*MT)
+// over the full K. kFast: K is a multiple of the chunk (2048/MT k), ring 4 steps deep; else
+// 128-k chunks and a one-step ring (small shapes).
+//
+// A chunk c+1 is loaded into registers (8 x 16 bytes per lane, whole 128-byte lines: lane l of
+// load i covers LDS bytes gi*1024 + 16*l of the chunk buffer, gi = 8i + wave) right after the
+// barrier that opens chunk c, and written to its LDS buffer at the end of chunk c, before the
+// next barrier. Plain loads keep the memory counter in order, so every wait the compiler places
+// for a weight step or for the staged chunk is exact; the chunk's loads are older than all
+// weight loads of chunk c and cost no wait at all by then.
+template <bool kGather, bool kSwiglu, int MT, bool kFast>
+__device__ void stream_tile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
+  constexpr int D = kFast ? kStreamDepth : 1;
+  constexpr int kFullChunk = kAChunk / (32 * MT);  // k-bytes per chunk
+  const int kc = kFast ? kFullChunk : 128;
+  const int spc = kc / 64;  // steps per chunk
+  const int nchunks = g.k / kc;
+  const int tid = opaque_tid();
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int units = g.n / kStreamUnit;
+  const int unit_raw = nb * kGemmWaves + wave;
+  const bool active = unit_raw < units;  // a partial column block leaves waves without columns
+  const int unit = active ? unit_raw : units - 1;
+
+  const int chunk_bytes = 32 * MT * kc;
+  const uint8_t* asrc[kALoads];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = mt * 32 + (lane & 31);
-    ap[mt] = a_row_ptr<kGather>(g, row0 + (r < mrows ? r : 0)) + (lane >> 5) * 32;
+  for (int i = 0; i < kALoads; ++i) {
+    const int pos = (i * kGemmWaves + wave) * 1024 + lane * 16;
+    const int r = pos / kc;
+    const int p = swizzle_piece((pos - r * kc) >> 4, r);
+    asrc[i] = a_row_ptr<kGather>(g, row0 + (r < mrows ? r : 0)) + p * 16;
   }
+  int4 astage[kALoads];
+  auto load_chunk = [&](int chunk) {
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i)
+      if (kFast || (i * kGemmWaves + wave) * 1024 < chunk_bytes)
+        astage[i] = ld16(asrc[i] + static_cast<int64_t>(chunk) * kc);
+  };
+  auto store_chunk = [&](int chunk) {
+    uint8_t* dst = smem + (chunk & 1) * kAChunk + wave * 1024 + lane * 16;
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i)
+      if (kFast || (i * kGemmWaves + wave) * 1024 < chunk_bytes)
+        *reinterpret_cast<int4*>(dst + i * kGemmWaves * 1024) = astage[i];
+  };
+  // operand reads: lane l is row l%32 (+32 mt), k-bytes [64j + 32*(l/32), +32) of chunk step j
+  const uint8_t* sbase = smem + (lane & 31) * kc;
+  const int hk = lane >> 5;
+  int pc[2][2];  // swizzled byte offset of piece 4v + 2hk + h within its 128-byte group
+#pragma unroll
+  for (int v = 0; v < 2; ++v)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) pc[v][h] = (((4 * v + 2 * hk + h) ^ lane) & 7) << 4;
+
   const uint8_t* bp[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
-    const int n = weight_row<kSwiglu>(g, nb, kStreamBN, ct * 32 + (lane & 31));
+    const int n = weight_row<kSwiglu>(g, unit, kStreamUnit, ct * 32 + (lane & 31));
     bp[ct] = g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) +
-             (n & 15) * 16 + (lane >> 5) * 512;
+             (n & 15) * 16 + hk * 512;
   }
-
-  int4 ar[kDepth][MT][2];
-  int4 br[kDepth][2][2];
-  auto issue = [&](int slot, int s) {
+  int4 br[D][2][2];  // [ring slot][column tile][16-byte half]
+  auto issue = [&](int d, int s) {
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-      br[slot][ct][0] = ld16(bp[ct] + static_cast<int64_t>(s) * 1024);
-      br[slot][ct][1] = ld16(bp[ct] + static_cast<int64_t>(s) * 1024 + 256);
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      ar[slot][mt][0] = ld16(ap[mt] + s * 64);
-      ar[slot][mt][1] = ld16(ap[mt] + s * 64 + 16);
+      const uint8_t* p = bp[ct] + static_cast<int64_t>(s) * 1024;
+      br[d][ct][0] = ld16(p);
+      br[d][ct][1] = ld16(p + 256);
     }
   };
   v16f acc[MT][2];
@@ -152,112 +260,101 @@ __device__ void stream_wave_tile(const GemmArgs& g, int e, int row0, int mrows, 
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mt][ct][v] = 0.0f;
-  auto compute = [&](int slot) {
-    const v8i b0 = make_v8i(br[slot][0][0], br[slot][0][1]);
-    const v8i b1 = make_v8i(br[slot][1][0], br[slot][1][1]);
+  // step j of chunk c (j & 1 is a compile-time constant in the unrolled loops below)
+  auto compute = [&](int d, int c, int j) {
+    const v8i b0 = make_v8i(br[d][0][0], br[d][0][1]);
+    const v8i b1 = make_v8i(br[d][1][0], br[d][1][1]);
+    const uint8_t* base = sbase + (c & 1) * kAChunk + (j >> 1) * 128;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const v8i a = make_v8i(ar[slot][mt][0], ar[slot][mt][1]);
+      const uint8_t* rb = base + mt * 32 * kc;
+      const v8i a = make_v8i(*reinterpret_cast<const int4*>(rb + pc[j & 1][0]),
+                             *reinterpret_cast<const int4*>(rb + pc[j & 1][1]));
       acc[mt][0] = mfma_fp8(a, b0, acc[mt][0]);
       acc[mt][1] = mfma_fp8(a, b1, acc[mt][1]);
     }
   };
-  if (nsteps >= kDepth && nsteps % kDepth == 0) {
+
+  load_chunk(0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-      issue(d, d);
-      __builtin_amdgcn_sched_barrier(0);
+  for (int d = 0; d < D; ++d) {
+    issue(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  store_chunk(0);
+  lds_barrier();
+  for (int c = 0; c + 1 < nchunks; ++c) {
+    load_chunk(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < spc; j += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        compute(d, c, j + d);
+        issue(d, c * spc + j + d + D);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    for (int i = 0; i + kDepth < nsteps; i += kDepth) {
+    store_chunk(c + 1);  // its buffer was last read in chunk c - 1, before the last barrier
+    lds_barrier();
+  }
+  {
+    const int c = nchunks - 1;
+    for (int j = 0; j + D < spc; j += D) {
 #pragma unroll
-      for (int d = 0; d < kDepth; ++d) {
-        compute(d);
-        issue(d, i + d + kDepth);
+      for (int d = 0; d < D; ++d) {
+        compute(d, c, j + d);
+        issue(d, c * spc + j + d + D);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) compute(d);
-  } else {
-    for (int s = 0; s < nsteps; ++s) {  // short K (small shapes): one step at a time
-      issue(0, s);
-      compute(0);
-    }
+    for (int d = 0; d < D; ++d) compute(d, c, spc - D + d);
   }
 
-  if (!kSwiglu) {
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) {
-      const int col = nb * kStreamBN + ct * 32 + (lane & 31);
-      const float bs = g.b_scale[static_cast<int64_t>(e) * g.n + col];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int r = mt * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-          if (r < mrows) {
-            const int row = row0 + r;
-            g.c[static_cast<int64_t>(row) * g.n + col] =
-                f32_to_bf16(acc[mt][ct][v] * row_scale<kGather>(g, row) * bs);
-          }
-        }
-    }
-  } else {
-    const int chan = nb * (kStreamBN / 2) + (lane & 31);
-    const float wsg = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
-    const float wsu = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = mt * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        const bool ok = r < mrows;
-        const int row = row0 + (ok ? r : 0);
-        float yv = 0.0f;
-        if (ok) {
-          yv = swiglu_value(g, acc[mt][0][v], acc[mt][1][v], row_scale<kGather>(g, row), wsg, wsu,
-                            g.sw.row_weight[row]);
-          g.sw.y[static_cast<int64_t>(row) * g.sw.inter + chan] = yv;
-        }
-        const float m = half_wave_max(fabsf(yv));
-        if (ok && (lane & 31) == 0) atomicMax(g.sw.amax + row, __float_as_uint(m));
-      }
-  }
+  if (!active) return;
+  store_tile<kGather, kSwiglu, MT>(g, acc, e, row0, mrows, unit);
 }
 
 // ------------------------------------------------------------------ TILE engine
+// One 128x128 tile computed by a 4-wave half of the workgroup (local thread id tid, LDS half
+// smem). Both halves run the same number of k steps, so their barriers pair up; a half without
+// a tile (active == false) runs the loop on zeros and stores nothing.
 template <bool kGather, bool kSwiglu>
-__device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem) {
+__device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int nb, uint8_t* smem,
+                          int tid_in, bool active) {
   constexpr int BM = kTileBM, BN = kTileBN, BK = kTileBK;
   constexpr int KB = BK / 16;
-  constexpr int kAPer = BM * BK / 16 / kGemmThreads;
-  constexpr int kBPer = BN * BK / 16 / kGemmThreads;
+  constexpr int kAPer = BM * BK / 16 / kTileThreads;
+  constexpr int kBPer = BN * BK / 16 / kTileThreads;
   constexpr int kStage = (BM + BN) * BK;
   constexpr int WTM = BM / kTileWM, WTN = BN / kTileWN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  const int tid = threadIdx.x;
-  const int lane = lane_id();
+  const int tid = opaque_tid() & (kTileThreads - 1);
+  const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
+  (void)tid_in;
   const int wm = wave / kTileWN, wn = wave % kTileWN;
   const int k_steps = g.k / BK;
 
   const uint8_t* a_src[kAPer];
 #pragma unroll
   for (int i = 0; i < kAPer; ++i) {
-    const int c = tid + i * kGemmThreads;
+    const int c = tid + i * kTileThreads;
     const int rb = c / (16 * KB);
     const int rem = c - rb * 16 * KB;
     const int r = rb * 16 + (rem & 15);
-    a_src[i] = r < mrows ? a_row_ptr<kGather>(g, row0 + r) + (rem >> 4) * 16 : nullptr;
+    a_src[i] = active && r < mrows ? a_row_ptr<kGather>(g, row0 + r) + (rem >> 4) * 16 : nullptr;
   }
   const uint8_t* b_src[kBPer];
 #pragma unroll
   for (int i = 0; i < kBPer; ++i) {
-    const int c = tid + i * kGemmThreads;
+    const int c = tid + i * kTileThreads;
     const int rb = c / (16 * KB);
     const int rem = c - rb * 16 * KB;
     const int n = weight_row<kSwiglu>(g, nb, BN, rb * 16);  // row-tile aligned
-    b_src[i] = g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) + rem * 16;
+    b_src[i] = active ? g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) + rem * 16
+                      : nullptr;
   }
   int4 ra[kAPer];
   int4 rbv[kBPer];
@@ -265,15 +362,16 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int nb,
 #pragma unroll
     for (int i = 0; i < kAPer; ++i) ra[i] = a_src[i] != nullptr ? ld16(a_src[i] + k0) : make_int4(0, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < kBPer; ++i) rbv[i] = ld16(b_src[i] + static_cast<int64_t>(k0) * 16);
+    for (int i = 0; i < kBPer; ++i)
+      rbv[i] = b_src[i] != nullptr ? ld16(b_src[i] + static_cast<int64_t>(k0) * 16) : make_int4(0, 0, 0, 0);
   };
   auto store_stage = [&](int buf) {
     uint8_t* sa = smem + buf * kStage;
     uint8_t* sb = sa + BM * BK;
 #pragma unroll
-    for (int i = 0; i < kAPer; ++i) *reinterpret_cast<int4*>(sa + (tid + i * kGemmThreads) * 16) = ra[i];
+    for (int i = 0; i < kAPer; ++i) *reinterpret_cast<int4*>(sa + (tid + i * kTileThreads) * 16) = ra[i];
 #pragma unroll
-    for (int i = 0; i < kBPer; ++i) *reinterpret_cast<int4*>(sb + (tid + i * kGemmThreads) * 16) = rbv[i];
+    for (int i = 0; i < kBPer; ++i) *reinterpret_cast<int4*>(sb + (tid + i * kTileThreads) * 16) = rbv[i];
   };
 
   v16f acc[TM][TN];
@@ -324,83 +422,53 @@ __device__ void tile_tile(const GemmArgs& g, int e, int row0, int mrows, int nb,
     if (kt + 1 < k_steps) store_stage(cur ^ 1);
     __syncthreads();
   }
-
-  if (!kSwiglu) {
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = wm * WTM + tm * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (r < mrows) {
-          const int row = row0 + r;
-          const float sa = row_scale<kGather>(g, row);
-          uint16_t* crow = g.c + static_cast<int64_t>(row) * g.n;
-#pragma unroll
-          for (int tn = 0; tn < TN; ++tn) {
-            const int col = nb * BN + b_col(tn) + (lane & 31);
-            crow[col] = f32_to_bf16(acc[tm][tn][v] * sa * g.b_scale[static_cast<int64_t>(e) * g.n + col]);
-          }
-        }
-      }
-    }
-  } else {
-    static_assert(TN == 2, "SwiGLU epilogue pairs one gate and one up column tile");
-    const int chan = nb * (BN / 2) + wn * 32 + (lane & 31);
-    const float wsg = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
-    const float wsu = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = wm * WTM + tm * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        const bool ok = r < mrows;
-        const int row = row0 + (ok ? r : 0);
-        float yv = 0.0f;
-        if (ok) {
-          yv = swiglu_value(g, acc[tm][0][v], acc[tm][1][v], row_scale<kGather>(g, row), wsg, wsu,
-                            g.sw.row_weight[row]);
-          g.sw.y[static_cast<int64_t>(row) * g.sw.inter + chan] = yv;
-        }
-        const float m = half_wave_max(fabsf(yv));
-        if (ok && (lane & 31) == 0) atomicMax(g.sw.amax + row, __float_as_uint(m));
-      }
-    }
-  }
+  if (!active) return;
+  static_assert(TN == 2 && WTN == 2 * 32, "a wave's tile is 64 columns: SwiGLU pairs gate and up");
+  store_tile<kGather, kSwiglu, TM>(g, acc, e, row0 + wm * WTM, mrows - wm * WTM, nb * kTileWN + wn);
 }
 
-// ------------------------------------------------------------------ persistent dispatchers
-// Wave 0 of the workgroup fills s_prefix[0..E] with the exclusive prefix of the tiles of the
-// experts this kernel owns (`tile_kernel`: experts on the TILE engine, else STREAM).
-__device__ void enumerate_tiles(const GemmArgs& g, bool tile_kernel, int* s_prefix) {
+// ------------------------------------------------------------------ persistent dispatcher
+__device__ __forceinline__ int stream_blocks(const GemmArgs& g) {
+  return (g.n / kStreamUnit + kGemmWaves - 1) / kGemmWaves;
+}
+
+// Wave 0 fills s_prefix[0..E] with the exclusive prefix of the workgroup work items of the
+// experts, s_tile[e] with the expert's engine (1 = TILE) and s_count[e] with its routed rows.
+// A STREAM item is one (64-row chunk, 512-column block); a TILE item is a pair of 128x128
+// tiles of the expert (row-block major).
+__device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, int* s_count) {
   const int E = g.num_experts;
   const int lane = lane_id();
+  const int stream_nb = stream_blocks(g);
+  const int tile_nb = g.n / kTileBN;
   if (threadIdx.x < kWave) {
     int carry = 0;
     for (int e0 = 0; e0 < E; e0 += kWave) {
       const int e = e0 + lane;
-      int tiles = 0;
+      int items = 0;
       if (e < E) {
         const int cnt = g.counts[e];
         const bool tile = g.engine == GemmEngine::kTile ||
-                          (g.engine == GemmEngine::kAuto && cnt > kStreamMaxRows);
-        if (tile == tile_kernel)
-          tiles = tile ? (cnt + kTileBM - 1) / kTileBM * (g.n / kTileBN)
-                       : (cnt + kStreamMaxRows - 1) / kStreamMaxRows * (g.n / kStreamBN);
+                          (g.engine == GemmEngine::kAuto && cnt > kStreamRows);
+        items = tile ? ((cnt + kTileBM - 1) / kTileBM * tile_nb + 1) / 2
+                     : (cnt + kStreamRows - 1) / kStreamRows * stream_nb;
+        s_tile[e] = tile;
+        s_count[e] = cnt;
       }
-      int inc = tiles;
+      int inc = items;
 #pragma unroll
       for (int off = 1; off < kWave; off <<= 1) {
         const int u = __shfl_up(inc, off, kWave);
         if (lane >= off) inc += u;
       }
-      if (e < E) s_prefix[e] = carry + inc - tiles;
+      if (e < E) s_prefix[e] = carry + inc - items;
       carry += __shfl(inc, kWave - 1, kWave);
     }
     if (lane == 0) s_prefix[E] = carry;
   }
 }
 
-__device__ __forceinline__ int expert_of_tile(const int* s_prefix, int E, int t) {
+__device__ __forceinline__ int expert_of_item(const int* s_prefix, int E, int t) {
   int lo = 0, hi = E;  // last e with s_prefix[e] <= t
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
@@ -410,70 +478,74 @@ __device__ __forceinline__ int expert_of_tile(const int* s_prefix, int E, int t)
 }
 
 template <bool kGather, bool kSwiglu>
-__global__ __launch_bounds__(kWave, 2) void stream_gemm_kernel(GemmArgs g) {
-  __shared__ int s_prefix[kMaxGemmExperts + 1];
-  enumerate_tiles(g, false, s_prefix);
-  __syncthreads();
-  const int E = g.num_experts;
-  const int total = s_prefix[E];
-  const int nt = g.n / kStreamBN;
-  for (int t = blockIdx.x; t < total; t += gridDim.x) {
-    const int e = expert_of_tile(s_prefix, E, t);
-    const int local = t - s_prefix[e];
-    const int mt = local / nt;
-    const int nb = local - mt * nt;
-    const int row0 = g.offsets[e] + mt * kStreamMaxRows;
-    const int mrows = min(kStreamMaxRows, g.counts[e] - mt * kStreamMaxRows);
-    if (mrows > 32)
-      stream_wave_tile<kGather, kSwiglu, 2>(g, e, row0, mrows, nb);
-    else
-      stream_wave_tile<kGather, kSwiglu, 1>(g, e, row0, mrows, nb);
-  }
-}
-
-template <bool kGather, bool kSwiglu>
-__global__ __launch_bounds__(kGemmThreads, 2) void tile_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_prefix[kMaxGemmExperts + 1];
-  enumerate_tiles(g, true, s_prefix);
+  __shared__ int s_tile[kMaxGemmExperts];
+  __shared__ int s_count[kMaxGemmExperts];
+  plan_items(g, s_prefix, s_tile, s_count);
   __syncthreads();
   const int E = g.num_experts;
   const int total = s_prefix[E];
-  const int nt = g.n / kTileBN;
+  const int stream_nb = stream_blocks(g);
+  const int tile_nb = g.n / kTileBN;
+  const bool fast1 = g.k % (kAChunk / 32) == 0;
+  const bool fast2 = g.k % (kAChunk / 64) == 0;
   for (int t = blockIdx.x; t < total; t += gridDim.x) {
-    const int e = expert_of_tile(s_prefix, E, t);
+    const int e = expert_of_item(s_prefix, E, t);
     const int local = t - s_prefix[e];
-    const int mt = local / nt;
-    const int nb = local - mt * nt;
-    tile_tile<kGather, kSwiglu>(g, e, g.offsets[e] + mt * kTileBM,
-                                min(kTileBM, g.counts[e] - mt * kTileBM), nb, smem);
+    const int cnt = s_count[e];
+    if (s_tile[e]) {
+      const int half = static_cast<int>(threadIdx.x) / kTileThreads;
+      const int ntiles = (cnt + kTileBM - 1) / kTileBM * tile_nb;
+      const int ti = 2 * local + half;
+      const bool active = ti < ntiles;
+      const int tt = active ? ti : ti - 1;
+      const int mt = tt / tile_nb;
+      const int nb = tt - mt * tile_nb;
+      tile_tile<kGather, kSwiglu>(g, e, g.offsets[e] + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM),
+                                  nb, smem + half * kTileSmem,
+                                  static_cast<int>(threadIdx.x) % kTileThreads, active);
+    } else {
+      const int mc = local / stream_nb;
+      const int nb = local - mc * stream_nb;
+      const int row0 = g.offsets[e] + mc * kStreamRows;
+      const int mrows = min(kStreamRows, cnt - mc * kStreamRows);
+      if (mrows > 32) {
+        if (fast2) stream_tile<kGather, kSwiglu, 2, true>(g, e, row0, mrows, nb, smem);
+        else stream_tile<kGather, kSwiglu, 2, false>(g, e, row0, mrows, nb, smem);
+      } else {
+        if (fast1) stream_tile<kGather, kSwiglu, 1, true>(g, e, row0, mrows, nb, smem);
+        else stream_tile<kGather, kSwiglu, 1, false>(g, e, row0, mrows, nb, smem);
+      }
+    }
     __syncthreads();
   }
 }
 
 template <bool kGather, bool kSwiglu>
 hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
-  if (g.engine != GemmEngine::kTile) {
-    const int64_t tiles =
-        (static_cast<int64_t>(max_rows) / kStreamMaxRows + g.num_experts) * (g.n / kStreamBN);
-    int64_t grid = static_cast<int64_t>(num_cus) * 8;  // 2 waves per SIMD
-    if (grid > tiles) grid = tiles;
-    hipLaunchKernelGGL((stream_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kWave), 0, stream, g);
-    const hipError_t err = hipGetLastError();
+  static bool attr_set = false;  // the 128 KB of dynamic LDS exceeds the default limit
+  if (!attr_set) {
+    const hipError_t err =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<kGather, kSwiglu>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes);
     if (err != hipSuccess) return err;
+    attr_set = true;
   }
-  if (g.engine != GemmEngine::kStream) {
-    const int64_t tiles =
-        (static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * (g.n / kTileBN);
-    int64_t grid = static_cast<int64_t>(num_cus) * 2;
-    if (grid > tiles) grid = tiles;
-    hipLaunchKernelGGL((tile_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
-                       dim3(kGemmThreads), kSmemBytes, stream, g);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-  }
-  return hipSuccess;
+  // upper bound of the work items over any split of max_rows rows into the experts
+  const int64_t stream_nb = (g.n / kStreamUnit + kGemmWaves - 1) / kGemmWaves;
+  const int64_t stream_items = (static_cast<int64_t>(max_rows) / kStreamRows + g.num_experts) * stream_nb;
+  const int64_t tile_items =
+      ((static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * (g.n / kTileBN) + g.num_experts) / 2 + 1;
+  const int64_t bound = g.engine == GemmEngine::kStream ? stream_items
+                        : g.engine == GemmEngine::kTile ? tile_items
+                                                        : std::max(stream_items, tile_items);
+  int64_t grid = num_cus;  // one 8-wave workgroup per CU
+  if (grid > bound) grid = bound;
+  hipLaunchKernelGGL((grouped_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kGemmThreads), kSmemBytes, stream, g);
+  return hipGetLastError();
 }
 
 }  // namespace

@@ -29,7 +29,6 @@ struct RouteArgs {
   int32_t* row_token;             // [rows]
   float* row_weight;              // [rows] or null
   int32_t* m_indices;             // [rows] or null
-  uint32_t* row_amax;             // [rows] or null: per-row |y| max of the fused GEMM1, cleared here
 };
 
 // Count -> offsets -> stable scatter over at most max_tasks = S*K tasks. Deterministic: rows
@@ -40,13 +39,12 @@ hipError_t launch_route(const RouteArgs& a, int64_t max_tasks, hipStream_t strea
 // (weight streaming, decode) and TILE otherwise (128x128 MFMA tiles, prefill).
 enum class GemmEngine : int { kAuto = 0, kStream = 1, kTile = 2 };
 
-// Fused GEMM1 epilogue: SwiGLU x route weight -> fp32 y and the per-row |y| max.
+// Fused GEMM1 epilogue: SwiGLU x route weight -> fp32 y.
 struct SwigluEpilogue {
   int enabled;
   int inter;                // I: gate weight rows [0, I), up rows [I, 2I)
   const float* row_weight;  // [rows] top-k weight of each routed row
   float* y;                 // f32 [rows, I] SwiGLU output (before requant)
-  uint32_t* amax;           // [rows] float bits of max |y| (atomic max; cleared by the route)
   int has_clamp;
   float clamp;
 };
@@ -74,9 +72,9 @@ struct GemmArgs {
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream);
 bool gemm_shape_supported(int n, int k);
 
-// Per-row requant of the SwiGLU output with its row max: a = max(amax, 1e-4);
+// Per-row requant of the SwiGLU output: amax = max |y| (written out), a = max(amax, 1e-4);
 // act = e4m3(clip(y * 448/a)); act_scale = a/448 -- for rows < meta[0].
-hipError_t launch_requant(const float* y, const uint32_t* amax, const int32_t* meta,
+hipError_t launch_requant(const float* y, float* amax, const int32_t* meta,
                           uint8_t* act, float* act_scale, int64_t max_rows, int inter,
                           int num_cus, hipStream_t stream);
 

@@ -99,7 +99,6 @@ __device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t ta
     a.row_token[row] = static_cast<int32_t>(task / a.topk);
     if (a.row_weight != nullptr) a.row_weight[row] = w;
     if (a.m_indices != nullptr) a.m_indices[row] = e;
-    if (a.row_amax != nullptr) a.row_amax[row] = 0u;
   }
 }
 
