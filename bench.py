@@ -62,6 +62,25 @@ def algorithmic_bytes(rows: int, touched: int) -> dict:
     return dict(layer=layer, gemm1=gemm1, gemm2=gemm2)
 
 
+PROFILE_KERNELS = {"gemm1": "grouped_gemm_kernel<true, true>",
+                   "gemm2": "grouped_gemm_kernel<false, false>"}
+
+
+def profiled_traffic(config_id: str, kernel: str):
+    """HBM bytes per dispatch of `kernel` measured by the two rocprofv3 --pmc passes
+    (FETCH_SIZE, WRITE_SIZE, calibrated on a plain copy) recorded in
+    profiles/megamoe_layer_<config>_*.md, or None when that config has no profile."""
+    import glob
+
+    name = PROFILE_KERNELS[kernel]
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"megamoe_layer_{config_id}_*.md"))):
+        for line in open(path):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) == 4 and cells[0] == name and cells[3].isdigit():
+                return int(cells[3]), os.path.relpath(path, ROOT)
+    return None
+
+
 def make_inputs(cfg: dict, torch, mm):
     """Seeded synthetic inputs drawn on the GPU (seed 1234 + config id)."""
     seed = 1234 + cfg["id"]
@@ -235,19 +254,23 @@ def main() -> int:
         stage_ms["gemm1"] = stage_ms.pop("gemm1_swiglu")
         dom = max(("gemm1", "gemm2"), key=lambda k: stage_ms[k])
         dom_s = stage_ms[dom] * 1e-3
+        prof = profiled_traffic(args.config, dom)
+        traffic = prof[0] if prof else None
         if bound == "hbm":
             achieved = nbytes[dom] / dom_s / 1e9
             roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1),
                             peak=HBM_PEAK_BPS / 1e9, unit="GB/s",
-                            frac=round(achieved * 1e9 / HBM_PEAK_BPS, 4), traffic=None,
-                            algorithmic_bytes=nbytes[dom], avg_us=round(stage_ms[dom] * 1e3, 2))
+                            frac=round(achieved * 1e9 / HBM_PEAK_BPS, 4), traffic=traffic,
+                            algorithmic_bytes=nbytes[dom], avg_us=round(stage_ms[dom] * 1e3, 2),
+                            traffic_source=prof[1] if prof else None)
         else:
             kflops = 2.0 * rows * HIDDEN * (2 * INTER if dom == "gemm1" else INTER)
             achieved = kflops / dom_s / 1e12
             roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 1),
                             peak=FP8_PEAK_FLOPS / 1e12, unit="TFLOP/s",
-                            frac=round(achieved * 1e12 / FP8_PEAK_FLOPS, 4), traffic=None,
-                            algorithmic_flops=kflops, avg_us=round(stage_ms[dom] * 1e3, 2))
+                            frac=round(achieved * 1e12 / FP8_PEAK_FLOPS, 4), traffic=traffic,
+                            algorithmic_flops=kflops, avg_us=round(stage_ms[dom] * 1e3, 2),
+                            traffic_source=prof[1] if prof else None)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -592,6 +592,8 @@ def fp8_mega_moe(
             raise ValueError("dispatch_num_tokens must be in "
                              f"0..{int(sym_buffer.num_max_tokens_per_rank)}")
         schedule = _schedule_for_mode(mode)
+    if not fast_math:  # both reference paths refuse it (mega_moe_fused_hip.cu:87-91, large_opt.py:381)
+        raise RuntimeError("DCU MegaMoE W8A8 channelwise persistent fused path requires fast_math")
     _validate_layer_tensors(call_y, l1_weights, l2_weights, cumulative_local_expert_recv_stats,
                             sym_buffer, recipe, activation)
     _launch_layer(call_y, l1_weights, l2_weights, cumulative_local_expert_recv_stats, sym_buffer,

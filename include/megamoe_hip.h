@@ -83,7 +83,7 @@ typedef struct mmoe_scratch_layout {
   int64_t row_weight_offset;   /* f32   [rows] top-k weight of each routed row */
   int64_t m_indices_offset;    /* int32 [rows] local expert of each routed row */
   int64_t act_scale_offset;    /* f32   [rows] per-row FP8 scale of the SwiGLU output */
-  int64_t amax_offset;         /* u32   [rows] float bits of max |y| per row */
+  int64_t amax_offset;         /* f32   [rows] max |y| per row (written by the requant stage) */
   int64_t y_offset;            /* f32   [rows, I]  SwiGLU x weight output of GEMM1 */
   int64_t act_offset;          /* e4m3  [rows, I]  requantised SwiGLU output */
   int64_t part_offset;         /* bf16  [rows, H]  per-row GEMM2 output (combine partials) */
@@ -150,8 +150,8 @@ int mmoe_forward(const mmoe_forward_args* args, void* stream);
 
 /* Stages of mmoe_forward, in order; each reads what the earlier ones left in route_scratch. */
 #define MMOE_STAGE_ROUTE 0   /* counts, offsets, output_index, per-row tables, stats */
-#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I] + row max |y| */
-#define MMOE_STAGE_REQUANT 2 /* act e4m3 [R, I] + act_scale [R] */
+#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I] */
+#define MMOE_STAGE_REQUANT 2 /* row max |y| -> amax [R], act e4m3 [R, I], act_scale [R] */
 #define MMOE_STAGE_GEMM2 3   /* part bf16 [R, H] */
 #define MMOE_STAGE_COMBINE 4 /* y */
 

@@ -326,3 +326,33 @@ def test_deepep_pre_post_process(mm, cuda, ids_dtype):
                 v = v * w[ok, j].view(-1, 1)
             acc[ok] += v
         assert torch.equal(y.cpu(), acc.to(torch.bfloat16))
+
+
+def test_api_flag_and_tensor_errors(mm, cuda):
+    """The reference's flag and tensor checks raise the same exception types and messages
+    (megamoe/__init__.py:343-410, csrc/apis/mega_dcu.hpp:355-433, large_opt.py:381)."""
+    s, e, hdim, inter, k = 16, 4, 256, 128, 3
+    log("api flag/tensor errors")
+    x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=5)
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=6, mm=mm)
+    buf = mm.SymmBuffer(None, e, s, k, hdim, inter)
+    y = torch.empty((s, hdim), dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(RuntimeError, match="requires fast_math"):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, fast_math=False)
+    with pytest.raises(ValueError, match="choose only one"):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, big_fused_cuda_graph=True,
+                             stages_fused_cuda_graph=True)
+    with pytest.raises(ValueError, match="dispatch_num_tokens must be in"):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, dispatch_num_tokens=s + 1)
+    with pytest.raises(RuntimeError, match="recipe"):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, recipe=(1, 1, 64))
+    with pytest.raises(RuntimeError, match="swiglu only"):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, activation="gelu")
+    with pytest.raises(RuntimeError, match="y must be BF16"):
+        mm.fp8_w8a8_mega_moe(y.float(), l1, l2, buf)
+    with pytest.raises(RuntimeError, match="FP8 E4M3 L1 weights"):
+        mm.fp8_w8a8_mega_moe(y, (l1[0].view(torch.uint8), l1[1]), l2, buf)
+    # the layer still runs after the refusals
+    y2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y2.float()).all()
