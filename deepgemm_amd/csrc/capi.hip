@@ -273,7 +273,12 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   const int max_rows = a->num_tokens * a->num_topk;
   void* ws = a->route_scratch;
 
-  if (runs(MMOE_STAGE_ROUTE)) {
+  // Small task counts: GEMM1 routes in-kernel (one launch fewer, no single-workgroup routing
+  // latency); the routing kernels serve larger counts and a routing-only call.
+  const bool route_in_gemm1 = runs(MMOE_STAGE_ROUTE) && runs(MMOE_STAGE_GEMM1) &&
+                              max_rows <= mmoe::gemm_route_max_tasks() &&
+                              a->num_experts <= mmoe::gemm_route_max_experts();
+  if (runs(MMOE_STAGE_ROUTE) && !route_in_gemm1) {
     st = run_route(a, l, s);
     if (st != MMOE_OK) return st;
   }
@@ -299,6 +304,10 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   g1.sw.y = at<float>(ws, l.y_offset);
   g1.sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
   g1.sw.clamp = a->activation_clamp;
+  if (route_in_gemm1) {
+    g1.route_in_kernel = 1;
+    g1.route = forward_route_args(a, l);
+  }
   if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
@@ -312,6 +321,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   if (runs(MMOE_STAGE_GEMM2)) {
     mmoe::GemmArgs g2 = g1;
     memset(&g2.sw, 0, sizeof(g2.sw));
+    g2.route_in_kernel = 0;
     g2.a = at<uint8_t>(ws, l.act_offset);
     g2.row_token = nullptr;
     g2.a_scale = at<float>(ws, l.act_scale_offset);

@@ -64,6 +64,8 @@ struct GemmArgs {
   int k;
   GemmEngine engine;
   SwigluEpilogue sw;         // GEMM1 only (requires row_token); c is unused then
+  int route_in_kernel;       // GEMM1: route the tasks in the kernel (<= gemm_route_max_tasks())
+  RouteArgs route;           // the routing to do then (counts, offsets, row tables are written)
 };
 
 // Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
@@ -71,6 +73,9 @@ struct GemmArgs {
 // device from counts (max_rows bounds the grid only).
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream);
 bool gemm_shape_supported(int n, int k);
+// Largest task count (S*K) and expert count GEMM1 can route in-kernel.
+int gemm_route_max_tasks();
+int gemm_route_max_experts();
 
 // Per-row requant of the SwiGLU output: amax = max |y| (written out), a = max(amax, 1e-4);
 // act = e4m3(clip(y * 448/a)); act_scale = a/448 -- for rows < meta[0].

@@ -18,8 +18,7 @@
 //   * large: a count kernel (one workgroup per chunk, LDS histogram) and a scatter kernel
 //     (one workgroup per chunk) that rebuilds the expert offsets and its chunk base from the
 //     per-chunk counts itself, so no grid-wide barrier or separate scan launch is needed.
-#include "common.cuh"
-#include "kernels.h"
+#include "route_wave.cuh"
 
 namespace mmoe {
 
@@ -30,59 +29,6 @@ constexpr int kSmallWaves = kSmallThreads / kWave;
 constexpr int kSmallMaxExperts = 256;
 constexpr int kChunkThreads = 256;
 constexpr int kChunkWaves = kChunkThreads / kWave;
-
-// Expert of a task (or -1), from already-loaded id and weight.
-__device__ __forceinline__ int valid_expert(const RouteArgs& a, int64_t e, float w) {
-  if (e < 0 || e >= a.num_experts) return -1;
-  if (a.check_weight && w == 0.0f) return -1;
-  return static_cast<int>(e);
-}
-
-__device__ __forceinline__ uint64_t lanes_below() {
-  const int lane = lane_id();
-  return lane == 0 ? 0ull : (~0ull >> (kWave - lane));
-}
-
-// Loads P passes of 64 tasks starting at `begin` (task begin + p*64 + lane) into registers,
-// all loads issued before any is used (one memory round trip per batch).
-template <int P>
-__device__ __forceinline__ void wave_load(const RouteArgs& a, int64_t begin, int64_t end, int* ev,
-                                          float* wv) {
-  const int lane = lane_id();
-  int64_t ids[P];
-#pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int64_t task = begin + p * kWave + lane;
-    const bool ok = task < end;
-    const int64_t t = ok ? task : 0;
-    ids[p] = a.idx_i64 ? static_cast<const int64_t*>(a.topk_idx)[t]
-                       : static_cast<int64_t>(static_cast<const int32_t*>(a.topk_idx)[t]);
-    wv[p] = a.topk_w[t];
-    if (!ok) ids[p] = -1;
-  }
-#pragma unroll
-  for (int p = 0; p < P; ++p) ev[p] = valid_expert(a, ids[p], wv[p]);
-}
-
-// Lanes of the wave holding the same expert id as this lane (invalid lanes: none), from one
-// ballot per id bit: O(log2 E) wave votes, no loop over the distinct experts.
-__device__ __forceinline__ uint64_t match_expert(int e, int id_bits) {
-  const uint64_t valid = __ballot(e >= 0);
-  uint64_t m = valid;
-  for (int b = 0; b < id_bits; ++b) {
-    const uint64_t ones = __ballot(e >= 0 && ((e >> b) & 1));
-    m &= ((e >> b) & 1) ? ones : ~ones;
-  }
-  return e >= 0 ? m : 0ull;
-}
-
-// Adds the per-expert counts of one 64-task pass into cnt[e] (this wave's private row): the
-// lowest lane of every equal-expert group adds the group size.
-__device__ __forceinline__ void wave_count_pass(int e, int id_bits, int* cnt) {
-  const uint64_t m = match_expert(e, id_bits);
-  if (e >= 0 && (m & lanes_below()) == 0ull) cnt[e] += __popcll(m);
-  __builtin_amdgcn_wave_barrier();
-}
 
 // Assigns rows to one 64-task pass in task order; base[e] is this wave's running base.
 __device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t task, bool in_range,
@@ -112,8 +58,7 @@ __device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* 
                            Gap phase_gap) {
   int ev[kBatch];
   float wv[kBatch];
-  int id_bits = 0;
-  while ((1 << id_bits) < a.num_experts) ++id_bits;
+  const int id_bits = expert_id_bits(a.num_experts);
   for (int64_t b = begin; b < end; b += kBatch * kWave) {
     wave_load<kBatch>(a, b, end, ev, wv);
 #pragma unroll
