@@ -29,11 +29,11 @@
 //    buffered: chunk c+1 is in flight while chunk c is used, and one barrier per chunk (1-4 per
 //    tile) hands the buffers over. Loading A per wave in MFMA operand order (32 lines per
 //    instruction, re-read by every wave) made the A reads, not the weights, set the pace.
-//  * TILE engine (more rows: prefill, MFMA-bound). Each 4-wave half of the workgroup computes
-//    a 128x128 output tile, BK = 128, A and B staged through double-buffered LDS in 16-row x
-//    16-byte blocks (block (rb, kb) at (rb*BK/16 + kb)*256); a 32x32x64 MFMA operand of lane l
-//    (row l%32, k-half l/32) is two 16-byte reads of consecutive blocks, 16 lanes reading 256
-//    contiguous bytes (conflict-free).
+//  * TILE engine (more rows: prefill, MFMA-bound). A 256 x 256 output tile per workgroup, the
+//    8 waves as 2 x 4 with 128 x 64 each, K in 128-byte stages through double-buffered LDS
+//    (A rows XOR-swizzled, B in Marlin's own 256-byte blocks). The 256-wide tile halves the
+//    L2 bytes per FLOP of a 128-wide one, which at 4 waves per tile needed about the whole
+//    per-CU L2 bandwidth.
 // In both engines lane l supplies k-bytes [32*(l/32), 32*(l/32)+32) of each 64-k MFMA step for
 // A and B alike; any such bijection gives the same dot product, and both engines accumulate the
 // 64-k steps in the same order, so they produce the same bits.
@@ -56,12 +56,12 @@ constexpr int kStreamRows = 64;     // rows per workgroup tile (experts up to th
 constexpr int kStreamDepth = 4;     // 64-k weight steps in flight per wave
 constexpr int kAChunk = 65536;      // bytes of one A chunk buffer (32*MT rows x 2048/MT k)
 constexpr int kALoads = kAChunk / 1024 / kGemmWaves;  // 16-byte A loads per lane per chunk
-// TILE engine (per 4-wave half)
-constexpr int kTileThreads = 256;
-constexpr int kTileBM = 128, kTileBN = 128, kTileBK = 128;
-constexpr int kTileWM = 2, kTileWN = 2;
-constexpr int kTileSmem = 65536;
-constexpr int kSmemBytes = 2 * kAChunk;  // == 2 * kTileSmem
+// TILE engine: 256 x 256 output tile, BK = 128, the 8 waves as 2 (M) x 4 (N), each wave 128
+// rows x 64 columns (4 x 2 MFMA tiles of 32 x 32)
+constexpr int kTileBM = 256, kTileBN = 256, kTileBK = 128;
+constexpr int kTileWM = 2, kTileWN = 4;
+constexpr int kTileStage = (kTileBM + kTileBN) * kTileBK;  // 64 KB: A rows, then B row-tiles
+constexpr int kSmemBytes = 2 * kAChunk;  // == 2 * kTileStage
 
 __device__ __forceinline__ v8i make_v8i(const int4& lo, const int4& hi) {
   v8i r;
@@ -340,60 +340,65 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
 }
 
 // ------------------------------------------------------------------ TILE engine
-// One 128x128 tile computed by a 4-wave half of the workgroup (local thread id tid, LDS half
-// smem). Both halves run the same number of k steps, so their barriers pair up; a half without
-// a tile (active == false) runs the loop on zeros and stores nothing.
+// One 256 x 256 output tile (expert e, 256-column block nb, rows [row0, row0 + mrows)), K in
+// BK = 128 stages through double-buffered LDS: the next stage's global loads go out into
+// registers before the MFMAs of the current one and are written to the other LDS stage after
+// them (one barrier per stage). A stage holds A as 256 rows of 128 bytes, 16-byte piece p of
+// row r at piece p ^ (r % 8) (loaded as whole lines: 8 lanes per row), then B in Marlin's own
+// blocks (16 row-tiles x 8 k-blocks x 256 bytes: each row-tile's stage is 2 KB contiguous in
+// the weight, copied as is). A 32x32x64 operand is two 16-byte LDS reads per lane; 16 lanes
+// read 256 contiguous bytes of B, and 8 lanes read 8 distinct 16-byte bank groups of A.
 template <bool kGather, bool kSwiglu>
 __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
-                          uint8_t* smem, bool active) {
-  constexpr int BM = kTileBM, BN = kTileBN, BK = kTileBK;
-  constexpr int KB = BK / 16;
-  constexpr int kAPer = BM * BK / 16 / kTileThreads;
-  constexpr int kBPer = BN * BK / 16 / kTileThreads;
-  constexpr int kStage = (BM + BN) * BK;
-  constexpr int WTM = BM / kTileWM, WTN = BN / kTileWN;
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  const int tid = opaque_tid() & (kTileThreads - 1);
+                          uint8_t* smem) {
+  constexpr int BK = kTileBK;
+  constexpr int TM = kTileBM / kTileWM / 32, TN = kTileBN / kTileWN / 32;  // 4 x 2
+  constexpr int kALoads = kTileBM * BK / 16 / kGemmThreads;  // 4
+  constexpr int kBLoads = kTileBN * BK / 16 / kGemmThreads;  // 4
+  const int tid = opaque_tid();
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
   const int wm = wave / kTileWN, wn = wave % kTileWN;
   const int k_steps = g.k / BK;
+  const int units = g.n / kStreamUnit;            // 64-column units of the output
+  const int unit = nb * kTileWN + wn;             // this wave's unit
+  const int row_tiles = g.n / 16;                 // weight row-tiles of the expert
 
-  const uint8_t* a_src[kAPer];
+  // A: load i covers rows i*64 + tid/8, piece tid % 8 (whole 128-byte row lines)
+  const uint8_t* a_src[kALoads];
+  int a_dst[kALoads];
 #pragma unroll
-  for (int i = 0; i < kAPer; ++i) {
-    const int c = tid + i * kTileThreads;
-    const int rb = c / (16 * KB);
-    const int rem = c - rb * 16 * KB;
-    const int r = rb * 16 + (rem & 15);
-    a_src[i] = active && r < mrows ? a_row_ptr<kGather>(g, rs, row0 + r) + (rem >> 4) * 16 : nullptr;
+  for (int i = 0; i < kALoads; ++i) {
+    const int r = i * (kGemmThreads / 8) + (tid >> 3);
+    const int p = tid & 7;
+    a_src[i] = a_row_ptr<kGather>(g, rs, row0 + (r < mrows ? r : 0)) + p * 16;
+    a_dst[i] = r * BK + ((p ^ (r & 7)) << 4);
   }
-  const uint8_t* b_src[kBPer];
+  // B: load i covers byte q = (i*512 + tid)*16 of the stage's 16 row-tiles x 2 KB
+  const uint8_t* b_src[kBLoads];
 #pragma unroll
-  for (int i = 0; i < kBPer; ++i) {
-    const int c = tid + i * kTileThreads;
-    const int rb = c / (16 * KB);
-    const int rem = c - rb * 16 * KB;
-    const int n = weight_row<kSwiglu>(g, nb, BN, rb * 16);  // row-tile aligned
-    b_src[i] = active ? g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) + rem * 16
-                      : nullptr;
+  for (int i = 0; i < kBLoads; ++i) {
+    const int q = (i * kGemmThreads + tid) * 16;
+    const int rt = q >> 11;  // 2 KB per row-tile per stage
+    int n = weight_row<kSwiglu>(g, nb, kTileBN, rt * 16);
+    if ((n >> 4) >= row_tiles) n = 0;  // a partial column block: any valid row-tile
+    b_src[i] = g.b + (static_cast<int64_t>(e) * row_tiles + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) +
+               (q & 2047);
   }
-  int4 ra[kAPer];
-  int4 rbv[kBPer];
-  auto load_stage = [&](int k0) {
+  int4 ra[kALoads], rb[kBLoads];
+  auto load_stage = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < kAPer; ++i) ra[i] = a_src[i] != nullptr ? ld16(a_src[i] + k0) : make_int4(0, 0, 0, 0);
+    for (int i = 0; i < kALoads; ++i) ra[i] = ld16(a_src[i] + kt * BK);
 #pragma unroll
-    for (int i = 0; i < kBPer; ++i)
-      rbv[i] = b_src[i] != nullptr ? ld16(b_src[i] + static_cast<int64_t>(k0) * 16) : make_int4(0, 0, 0, 0);
+    for (int i = 0; i < kBLoads; ++i) rb[i] = ld16(b_src[i] + static_cast<int64_t>(kt) * BK * 16);
   };
   auto store_stage = [&](int buf) {
-    uint8_t* sa = smem + buf * kStage;
-    uint8_t* sb = sa + BM * BK;
+    uint8_t* sa = smem + buf * kTileStage;
+    uint8_t* sb = sa + kTileBM * BK;
 #pragma unroll
-    for (int i = 0; i < kAPer; ++i) *reinterpret_cast<int4*>(sa + (tid + i * kTileThreads) * 16) = ra[i];
+    for (int i = 0; i < kALoads; ++i) *reinterpret_cast<int4*>(sa + a_dst[i]) = ra[i];
 #pragma unroll
-    for (int i = 0; i < kBPer; ++i) *reinterpret_cast<int4*>(sb + (tid + i * kTileThreads) * 16) = rbv[i];
+    for (int i = 0; i < kBLoads; ++i) *reinterpret_cast<int4*>(sb + (i * kGemmThreads + tid) * 16) = rb[i];
   };
 
   v16f acc[TM][TN];
@@ -404,28 +409,29 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  // B tile column of the wave's column tile tn: without SwiGLU wn*64 + tn*32; with SwiGLU the
-  // wave's gate columns (tn = 0) sit at wn*32 and the matching up columns (tn = 1) at 64+wn*32.
-  auto b_col = [&](int tn) { return kSwiglu ? tn * (BN / 2) + wn * 32 : wn * WTN + tn * 32; };
-
+  // B column of the wave's column tile tn: without SwiGLU wn*64 + tn*32; with SwiGLU the
+  // gate columns (tn = 0) at wn*32 and the matching up columns (tn = 1) at 128 + wn*32.
+  auto b_col = [&](int tn) { return kSwiglu ? tn * (kTileBN / 2) + wn * 32 : wn * 64 + tn * 32; };
+  const int hk = lane >> 5;
   auto compute_stage = [&](int buf) {
-    const uint8_t* sa = smem + buf * kStage;
-    const uint8_t* sb = sa + BM * BK;
+    const uint8_t* sa = smem + buf * kTileStage;
+    const uint8_t* sb = sa + kTileBM * BK;
 #pragma unroll
     for (int ks = 0; ks < BK / 64; ++ks) {
-      const int kb = ks * 4 + (lane >> 5) * 2;
+      const int p0 = ks * 4 + hk * 2;
       v8i av[TM], bv[TN];
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm) {
-        const int r = wm * WTM + tm * 32 + (lane & 31);
-        const int off = ((r >> 4) * KB + kb) * 256 + (r & 15) * 16;
-        av[tm] = make_v8i(*reinterpret_cast<const int4*>(sa + off), *reinterpret_cast<const int4*>(sa + off + 256));
+        const int r = wm * (TM * 32) + tm * 32 + (lane & 31);
+        const uint8_t* ar = sa + r * BK;
+        av[tm] = make_v8i(*reinterpret_cast<const int4*>(ar + ((p0 ^ (r & 7)) << 4)),
+                          *reinterpret_cast<const int4*>(ar + (((p0 + 1) ^ (r & 7)) << 4)));
       }
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
-        const int cidx = b_col(tn) + (lane & 31);
-        const int off = ((cidx >> 4) * KB + kb) * 256 + (cidx & 15) * 16;
-        bv[tn] = make_v8i(*reinterpret_cast<const int4*>(sb + off), *reinterpret_cast<const int4*>(sb + off + 256));
+        const int c = b_col(tn) + (lane & 31);
+        const uint8_t* bc = sb + (c >> 4) * (BK * 16) + p0 * 256 + (c & 15) * 16;
+        bv[tn] = make_v8i(*reinterpret_cast<const int4*>(bc), *reinterpret_cast<const int4*>(bc + 256));
       }
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
@@ -439,14 +445,19 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   __syncthreads();
   for (int kt = 0; kt < k_steps; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < k_steps) load_stage((kt + 1) * BK);
+    if (kt + 1 < k_steps) load_stage(kt + 1);
     compute_stage(cur);
     if (kt + 1 < k_steps) store_stage(cur ^ 1);
     __syncthreads();
   }
-  if (!active) return;
-  static_assert(TN == 2 && WTN == 2 * 32, "a wave's tile is 64 columns: SwiGLU pairs gate and up");
-  store_tile<kGather, kSwiglu, TM>(g, rs, acc, e, row0 + wm * WTM, mrows - wm * WTM, nb * kTileWN + wn);
+  if (unit >= units) return;
+  static_assert(TN == 2 && TM == 4, "a wave's tile is 128 rows x 64 columns");
+  const int wrow = row0 + wm * (TM * 32);
+  const int wrows = mrows - wm * (TM * 32);
+  store_tile<kGather, kSwiglu, 2>(g, rs, *reinterpret_cast<const v16f(*)[2][2]>(&acc[0]), e, wrow,
+                                  wrows, unit);
+  store_tile<kGather, kSwiglu, 2>(g, rs, *reinterpret_cast<const v16f(*)[2][2]>(&acc[2]), e, wrow + 64,
+                                  wrows - 64, unit);
 }
 
 // ------------------------------------------------------------------ in-kernel routing
@@ -463,7 +474,7 @@ constexpr int kFusedPasses = 16;  // 64-task passes per wave
 constexpr int kFusedMaxTasks = kGemmWaves * kFusedPasses * kWave;
 constexpr int kFusedMaxExperts = 255;  // expert ids in a byte, 255 = invalid task
 constexpr int kFusedBatch = 8;         // passes whose loads are in flight together
-constexpr int kRowTable = 2 * kTileBM;  // LDS row table: 256 rows (two TILE halves)
+constexpr int kRowTable = kTileBM;  // LDS row table: one TILE's 256 rows
 
 __device__ __forceinline__ int fused_per_wave(int ntasks) {
   return (ntasks + kGemmWaves * kWave - 1) / (kGemmWaves * kWave) * kWave;
@@ -548,13 +559,13 @@ __device__ __forceinline__ int stream_blocks(const GemmArgs& g) {
 
 // Wave 0 fills s_prefix[0..E] with the exclusive prefix of the workgroup work items of the
 // experts and s_tile[e] with the expert's engine (1 = TILE), from the routed rows s_count[e].
-// A STREAM item is one (64-row chunk, 512-column block); a TILE item is a pair of 128x128
-// tiles of the expert (row-block major).
+// A STREAM item is one (64-row chunk, 512-column block); a TILE item is one 256 x 256 tile
+// (row-block major).
 __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const int* s_count) {
   const int E = g.num_experts;
   const int lane = lane_id();
   const int stream_nb = stream_blocks(g);
-  const int tile_nb = g.n / kTileBN;
+  const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
   if (threadIdx.x < kWave) {
     int carry = 0;
     for (int e0 = 0; e0 < E; e0 += kWave) {
@@ -564,7 +575,7 @@ __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const 
         const int cnt = s_count[e];
         const bool tile = g.engine == GemmEngine::kTile ||
                           (g.engine == GemmEngine::kAuto && cnt > kStreamRows);
-        items = tile ? ((cnt + kTileBM - 1) / kTileBM * tile_nb + 1) / 2
+        items = tile ? (cnt + kTileBM - 1) / kTileBM * tile_nb
                      : (cnt + kStreamRows - 1) / kStreamRows * stream_nb;
         s_tile[e] = tile;
       }
@@ -659,7 +670,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   __syncthreads();
   const int total = s_prefix[E];
   const int stream_nb = stream_blocks(g);
-  const int tile_nb = g.n / kTileBN;
+  const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
   const bool fast1 = g.k % (kAChunk / 32) == 0;
   const bool fast2 = g.k % (kAChunk / 64) == 0;
   // Items are dealt to the XCDs in contiguous ranges (workgroup b runs on XCD b % 8), so the
@@ -677,25 +688,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
     const int cnt = s_count[e];
     const int off_e = s_off[e];
     if (s_tile[e]) {
-      const int half = static_cast<int>(threadIdx.x) / kTileThreads;
-      const int ntiles = (cnt + kTileBM - 1) / kTileBM * tile_nb;
-      const int ti = 2 * local + half;
-      const bool active = ti < ntiles;
-      const int tt = active ? ti : ti - 1;
-      const int mt = tt / tile_nb;
-      const int nb = tt - mt * tile_nb;
+      const int mt = local / tile_nb;
+      const int nb = local - mt * tile_nb;
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
-        const int t0 = 2 * local, t1 = min(2 * local + 1, ntiles - 1);
-        const int mt0 = t0 / tile_nb, mt1 = t1 / tile_nb;
-        const bool w0 = t0 % tile_nb == 0, w1 = t1 != t0 && t1 % tile_nb == 0;
-        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, mt0 * kTileBM,
-                   w0 ? mt0 * kTileBM : 0, w0 ? mt0 * kTileBM + kTileBM : 0,
-                   w1 ? mt1 * kTileBM : 0, w1 ? mt1 * kTileBM + kTileBM : 0, s_task, s_tok, s_rw);
-        rs = RowSrc{s_tok, s_rw, off_e + mt0 * kTileBM};
+        const int r0 = mt * kTileBM;
+        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, r0, nb == 0 ? r0 : 0,
+                   nb == 0 ? r0 + kTileBM : 0, 0, 0, s_task, s_tok, s_rw);
+        rs = RowSrc{s_tok, s_rw, off_e + r0};
       }
       tile_tile<kGather, kSwiglu>(g, rs, e, off_e + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM),
-                                  nb, smem + half * kTileSmem, active);
+                                  nb, smem);
     } else {
       const int mc = local / stream_nb;
       const int nb = local - mc * stream_nb;
@@ -734,7 +737,7 @@ hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStrea
   const int64_t stream_nb = (g.n / kStreamUnit + kGemmWaves - 1) / kGemmWaves;
   const int64_t stream_items = (static_cast<int64_t>(max_rows) / kStreamRows + g.num_experts) * stream_nb;
   const int64_t tile_items =
-      ((static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * (g.n / kTileBN) + g.num_experts) / 2 + 1;
+      (static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * ((g.n + kTileBN - 1) / kTileBN);
   const int64_t bound = g.engine == GemmEngine::kStream ? stream_items
                         : g.engine == GemmEngine::kTile ? tile_items
                                                         : std::max(stream_items, tile_items);
