@@ -364,16 +364,16 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   const int unit = nb * kTileWN + wn;             // this wave's unit
   const int row_tiles = g.n / 16;                 // weight row-tiles of the expert
 
-  // A: load i covers rows i*64 + tid/8, piece tid % 8 (whole 128-byte row lines)
+  // A: load i covers rows i*64 + tid/8, piece tid % 8 (whole 128-byte row lines); stored at
+  // piece p ^ ((r / 2) % 8), so 16 consecutive rows at one k hit 16 distinct bank groups
   const uint8_t* a_src[kALoads];
-  int a_dst[kALoads];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) {
     const int r = i * (kGemmThreads / 8) + (tid >> 3);
-    const int p = tid & 7;
-    a_src[i] = a_row_ptr<kGather>(g, rs, row0 + (r < mrows ? r : 0)) + p * 16;
-    a_dst[i] = r * BK + ((p ^ (r & 7)) << 4);
+    a_src[i] = a_row_ptr<kGather>(g, rs, row0 + (r < mrows ? r : 0)) + (tid & 7) * 16;
   }
+  const int a_key = (tid >> 4) & 7;  // (r / 2) % 8 of every A row this thread stores
+  const int a_dst0 = (tid >> 3) * BK + (((tid & 7) ^ a_key) << 4);  // + i * 64 * BK
   // B: load i covers byte q = (i*512 + tid)*16 of the stage's 16 row-tiles x 2 KB
   const uint8_t* b_src[kBLoads];
 #pragma unroll
@@ -396,7 +396,8 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     uint8_t* sa = smem + buf * kTileStage;
     uint8_t* sb = sa + kTileBM * BK;
 #pragma unroll
-    for (int i = 0; i < kALoads; ++i) *reinterpret_cast<int4*>(sa + a_dst[i]) = ra[i];
+    for (int i = 0; i < kALoads; ++i)
+      *reinterpret_cast<int4*>(sa + a_dst0 + i * (kGemmThreads / 8) * BK) = ra[i];
 #pragma unroll
     for (int i = 0; i < kBLoads; ++i) *reinterpret_cast<int4*>(sb + (i * kGemmThreads + tid) * 16) = rb[i];
   };
@@ -413,30 +414,46 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   // gate columns (tn = 0) at wn*32 and the matching up columns (tn = 1) at 128 + wn*32.
   auto b_col = [&](int tn) { return kSwiglu ? tn * (kTileBN / 2) + wn * 32 : wn * 64 + tn * 32; };
   const int hk = lane >> 5;
+  const int rkey = ((lane & 31) >> 1) & 7;  // (r / 2) % 8 of this lane's A rows
+  // Operands are read one MFMA group ahead (double-buffered registers), so the LDS latency of
+  // the next A (or the next k-step's B) overlaps the MFMAs of the current one.
+  auto read_b = [&](const uint8_t* sb, int ks, v8i (&bv)[TN]) {
+    const int p0 = ks * 4 + hk * 2;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int c = b_col(tn) + (lane & 31);
+      const uint8_t* bc = sb + (c >> 4) * (BK * 16) + p0 * 256 + (c & 15) * 16;
+      bv[tn] = make_v8i(*reinterpret_cast<const int4*>(bc), *reinterpret_cast<const int4*>(bc + 256));
+    }
+  };
+  auto read_a = [&](const uint8_t* sa, int ks, int tm) {
+    const int p0 = ks * 4 + hk * 2;
+    const uint8_t* ar = sa + (wm * (TM * 32) + tm * 32 + (lane & 31)) * BK;
+    return make_v8i(*reinterpret_cast<const int4*>(ar + ((p0 ^ rkey) << 4)),
+                    *reinterpret_cast<const int4*>(ar + (((p0 + 1) ^ rkey) << 4)));
+  };
   auto compute_stage = [&](int buf) {
     const uint8_t* sa = smem + buf * kTileStage;
     const uint8_t* sb = sa + kTileBM * BK;
+    v8i bv[2][TN];
+    read_b(sb, 0, bv[0]);
+    v8i a_cur = read_a(sa, 0, 0);
 #pragma unroll
     for (int ks = 0; ks < BK / 64; ++ks) {
-      const int p0 = ks * 4 + hk * 2;
-      v8i av[TM], bv[TN];
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm) {
-        const int r = wm * (TM * 32) + tm * 32 + (lane & 31);
-        const uint8_t* ar = sa + r * BK;
-        av[tm] = make_v8i(*reinterpret_cast<const int4*>(ar + ((p0 ^ (r & 7)) << 4)),
-                          *reinterpret_cast<const int4*>(ar + (((p0 + 1) ^ (r & 7)) << 4)));
+        v8i a_next;
+        if (tm + 1 < TM) a_next = read_a(sa, ks, tm + 1);
+        else if (ks + 1 < BK / 64) {
+          read_b(sb, ks + 1, bv[(ks + 1) & 1]);
+          a_next = read_a(sa, ks + 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs below
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = mfma_fp8(a_cur, bv[ks & 1][tn], acc[tm][tn]);
+        __builtin_amdgcn_sched_barrier(0);
+        a_cur = a_next;
       }
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int c = b_col(tn) + (lane & 31);
-        const uint8_t* bc = sb + (c >> 4) * (BK * 16) + p0 * 256 + (c & 15) * 16;
-        bv[tn] = make_v8i(*reinterpret_cast<const int4*>(bc), *reinterpret_cast<const int4*>(bc + 256));
-      }
-#pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-        for (int tn = 0; tn < TN; ++tn) acc[tm][tn] = mfma_fp8(av[tm], bv[tn], acc[tm][tn]);
     }
   };
 
@@ -688,8 +705,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
     const int cnt = s_count[e];
     const int off_e = s_off[e];
     if (s_tile[e]) {
-      const int mt = local / tile_nb;
-      const int nb = local - mt * tile_nb;
+      // row blocks in groups of 4, columns inside a group, so that the consecutive items an
+      // XCD runs together form 4 x 8 tiles sharing A rows and B columns in its L2
+      const int mblocks = (cnt + kTileBM - 1) / kTileBM;
+      const int group = local / (4 * tile_nb);
+      const int in_group = local - group * 4 * tile_nb;
+      const int rows_in_group = min(4, mblocks - group * 4);
+      const int nb = in_group / rows_in_group;
+      const int mt = group * 4 + (in_group - nb * rows_in_group);
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
         const int r0 = mt * kTileBM;
