@@ -311,11 +311,12 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
+  // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU
   if (runs(MMOE_STAGE_REQUANT) &&
-      mmoe::launch_requant(at<float>(ws, l.y_offset), at<float>(ws, l.amax_offset),
-                           at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
-                           at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, cus,
-                           s) != hipSuccess)
+      mmoe::launch_requant(at<float>(ws, l.y_offset), mmoe::gemm_wide_selected(g1, max_rows), g1.sw,
+                           at<float>(ws, l.amax_offset), at<int32_t>(ws, l.meta_offset),
+                           at<uint8_t>(ws, l.act_offset), at<float>(ws, l.act_scale_offset),
+                           max_rows, a->intermediate, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
   if (runs(MMOE_STAGE_GEMM2)) {

@@ -33,6 +33,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
+// SwiGLU x route weight of one channel from the bf16-rounded gate g and up u: the clamp of the
+// staged K2 (u to [-c, c], g to <= c), then g * sigmoid(g) * u * w left to right with the
+// fast-math sigmoid of the reference's fused path (hardware exp2 and reciprocal:
+// deep_gemm/include/deep_gemm/common/mega_moe_dcu.cuh:89-98; the staged K2 uses __expf,
+// megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:328).
+__device__ __forceinline__ float swiglu_weighted(float g, float u, float w, bool has_clamp, float c) {
+  if (has_clamp) {
+    u = fminf(c, fmaxf(-c, u));
+    g = fminf(c, g);
+  }
+  constexpr float kLog2E = 1.4426950408889634f;
+  const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2E));
+  return g * sig * u * w;
+}
+
 __device__ __forceinline__ float clip_e4m3(float v) {
   return fminf(kE4m3Max, fmaxf(-kE4m3Max, v));
 }

@@ -18,30 +18,57 @@ constexpr int kEltWaves = kEltThreads / kWave;
 // One wave per row: amax = max |y|; a = max(amax, 1e-4); act = e4m3(clip(y * (448/a)));
 // act_scale = a/448 (the K2 requant, megamoe/dcu_megamoe_large_opt/K2_fused/
 // k2_fused_ext.cu:341-364). A row of up to kRequantGroups*4*64 channels stays in registers
-// between the reduction and the quantization; a longer one is read twice.
+// between the reduction and the quantization; a longer one is read twice. kFromH: y is made
+// here from GEMM1's bf16 pre-activation h (gate channels [0, I), up [I, 2I)) by the K2
+// SwiGLU x route weight (k2_fused_ext.cu:283-340) instead of being read as fp32.
 constexpr int kRequantGroups = 8;  // float4 groups per lane held in registers
 
 __device__ __forceinline__ float abs_max4(float m, const float4& v) {
   return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
 }
 
-__global__ __launch_bounds__(kEltThreads) void requant_kernel(const float* y, float* amax,
-                                                              const int32_t* meta, uint8_t* act,
-                                                              float* act_scale, int inter) {
+struct RequantArgs {
+  const void* src;  // f32 y [rows, I], or bf16 h [rows, 2I] (kFromH)
+  SwigluEpilogue sw;
+  float* amax;
+  int32_t* meta;
+  uint8_t* act;
+  float* act_scale;
+  int inter;
+};
+
+// channels 4q .. 4q+3 of row `row`
+template <bool kFromH>
+__device__ __forceinline__ float4 requant_load(const RequantArgs& r, int64_t row, int q, float w) {
+  if (!kFromH) return reinterpret_cast<const float4*>(static_cast<const float*>(r.src) + row * r.inter)[q];
+  const uint16_t* h = static_cast<const uint16_t*>(r.src) + row * 2 * r.inter;
+  const uint2 gb = reinterpret_cast<const uint2*>(h)[q];
+  const uint2 ub = reinterpret_cast<const uint2*>(h + r.inter)[q];
+  const bool c = r.sw.has_clamp;
+  const float cv = r.sw.clamp;
+  return make_float4(swiglu_weighted(bf16_to_f32(gb.x & 0xffff), bf16_to_f32(ub.x & 0xffff), w, c, cv),
+                     swiglu_weighted(bf16_to_f32(gb.x >> 16), bf16_to_f32(ub.x >> 16), w, c, cv),
+                     swiglu_weighted(bf16_to_f32(gb.y & 0xffff), bf16_to_f32(ub.y & 0xffff), w, c, cv),
+                     swiglu_weighted(bf16_to_f32(gb.y >> 16), bf16_to_f32(ub.y >> 16), w, c, cv));
+}
+
+template <bool kFromH>
+__global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
-  const int rows = meta[0];
-  const int groups = inter >> 2;
+  const int rows = r.meta[0];
+  const int groups = r.inter >> 2;
+  if (blockIdx.x == 0 && threadIdx.x == 0) r.meta[1] = kFromH ? 1 : 0;
   for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
-    const float4* yr = reinterpret_cast<const float4*>(y + static_cast<int64_t>(row) * inter);
-    uint32_t* ar = reinterpret_cast<uint32_t*>(act + static_cast<int64_t>(row) * inter);
+    const float w = kFromH ? r.sw.row_weight[row] : 0.0f;
+    uint32_t* ar = reinterpret_cast<uint32_t*>(r.act + static_cast<int64_t>(row) * r.inter);
     float m = 0.0f;
     if (groups <= kRequantGroups * kWave) {
       float4 v[kRequantGroups];
 #pragma unroll
       for (int i = 0; i < kRequantGroups; ++i) {
         const int q = lane + i * kWave;
-        v[i] = q < groups ? yr[q] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[i] = q < groups ? requant_load<kFromH>(r, row, q, w) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         m = abs_max4(m, v[i]);
       }
       m = wave_max(m);
@@ -52,17 +79,17 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(const float* y, fl
         if (q < groups) ar[q] = pack_e4m3x4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
       }
     } else {
-      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, yr[q]);
+      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, requant_load<kFromH>(r, row, q, w));
       m = wave_max(m);
       const float inv = kE4m3Max / fmaxf(m, kAmaxFloor);
       for (int q = lane; q < groups; q += kWave) {
-        const float4 v = yr[q];
+        const float4 v = requant_load<kFromH>(r, row, q, w);
         ar[q] = pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
       }
     }
     if (lane == 0) {
-      amax[row] = m;
-      act_scale[row] = fmaxf(m, kAmaxFloor) / kE4m3Max;
+      r.amax[row] = m;
+      r.act_scale[row] = fmaxf(m, kAmaxFloor) / kE4m3Max;
     }
   }
 }
@@ -225,14 +252,18 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 
 }  // namespace
 
-hipError_t launch_requant(const float* y, float* amax, const int32_t* meta,
-                          uint8_t* act, float* act_scale, int64_t max_rows, int inter,
-                          int num_cus, hipStream_t stream) {
+hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw, float* amax,
+                          int32_t* meta, uint8_t* act, float* act_scale, int64_t max_rows,
+                          int inter, int num_cus, hipStream_t stream) {
   if (max_rows <= 0) return hipSuccess;
   if (inter % 4) return hipErrorInvalidValue;
+  if (from_h && sw.row_weight == nullptr) return hipErrorInvalidValue;
+  const RequantArgs r{src, sw, amax, meta, act, act_scale, inter};
   const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 4);
-  hipLaunchKernelGGL(requant_kernel, dim3(grid), dim3(kEltThreads), 0, stream, y, amax, meta, act,
-                     act_scale, inter);
+  if (from_h)
+    hipLaunchKernelGGL(requant_kernel<true>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+  else
+    hipLaunchKernelGGL(requant_kernel<false>, dim3(grid), dim3(kEltThreads), 0, stream, r);
   return hipGetLastError();
 }
 

@@ -122,13 +122,8 @@ __device__ __forceinline__ int weight_row(const GemmArgs& g, int nb, int tile_co
 // SwiGLU of one (row, channel): h rounded to bf16 exactly like the staged K1 output.
 __device__ __forceinline__ float swiglu_value(const GemmArgs& g, float gacc, float uacc, float xs,
                                               float wsg, float wsu, float route_w) {
-  float gh = bf16_round(gacc * xs * wsg);
-  float uh = bf16_round(uacc * xs * wsu);
-  if (g.sw.has_clamp) {
-    uh = fminf(g.sw.clamp, fmaxf(-g.sw.clamp, uh));
-    gh = fminf(g.sw.clamp, gh);
-  }
-  return gh * (1.0f / (1.0f + expf(-gh))) * uh * route_w;
+  return swiglu_weighted(bf16_round(gacc * xs * wsg), bf16_round(uacc * xs * wsu), route_w,
+                         g.sw.has_clamp, g.sw.clamp);
 }
 
 // Thread index for an engine body, opaque to the optimizer: values derived from it are computed
@@ -477,6 +472,221 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
                                   wrows - 64, unit);
 }
 
+// ------------------------------------------------------------------ WIDE engine
+// The TILE engine's 256 x 256 tile for a 4-wave workgroup (one wave per SIMD: 512 registers a
+// lane, the 256 accumulators in AGPRs), used when every expert has many rows. Wave w owns the
+// 64-column unit nb*4 + w over all 256 rows (8 x 2 MFMA tiles), so each weight column is read
+// by one wave only: B goes straight from global memory into MFMA operand registers (Marlin
+// gives each lane 16 contiguous k-bytes of a weight row), four 64-k steps ahead in a register
+// ring, and never touches LDS. A goes through LDS in BK = 128 stages: 256 rows of 128 bytes,
+// 16-byte piece p of row r at piece p ^ ((r / 2) % 8) (16 consecutive rows at one k hit 16
+// distinct 16-byte bank groups), three stages deep, so the first A operand of a stage is read
+// before the barrier that ends the previous one and the MFMA pipe does not drain there.
+constexpr int kWideThreads = 256, kWideWaves = 4;
+constexpr int kWideBK = 128;
+constexpr int kWideStage = kTileBM * kWideBK;  // 32 KB of A
+constexpr int kWideBufs = 3;
+constexpr int kWideOut = kTileBM * 128;  // a wave's staged output tile (256 rows x 128 bytes)
+constexpr int kWideSmemBytes = kWideWaves * kWideOut > kWideBufs * kWideStage ? kWideWaves * kWideOut
+                                                                                 : kWideBufs * kWideStage;
+constexpr int kWideRing = 4;  // 64-k steps of B in registers
+constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that select it
+
+// Epilogue of a WIDE tile. The MFMAs run transposed (weights as the first operand), so lane
+// l holds token row tm*32 + l%32 and, per 32-column tile tn, the columns 8*(v/4) + 4*(l/32) +
+// v%4: four runs of 4 consecutive columns. The row scale is then one value per lane and row
+// tile, the column scales four 16-byte loads per column tile, and every 4 results become one
+// 8-byte bf16 write into the wave's own 32 KB of LDS (256 rows x 128 bytes, 16-byte piece p of
+// row r at piece p ^ ((r / 2) % 8): conflict-free both ways). The rows then leave as whole
+// 16-byte pieces, 8 rows per store instruction.
+// GEMM1 (kGemm1) writes the pre-activation h = bf16(acc * x_scale * w_scale) [rows, 2I] with
+// gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
+// bf16 partials.
+template <bool kGather, bool kGemm1>
+__device__ __forceinline__ void store_wide(const GemmArgs& g, const RowSrc& rs,
+                                           const v16f (&acc)[kTileBM / 32][2], int e, int row0,
+                                           int mrows, int unit, uint8_t* wlds) {
+  constexpr int TM = kTileBM / 32;
+  const int lane = opaque_tid() & (kWave - 1);
+  const int rl = lane & 31, hk = lane >> 5;
+  // column scales: tile tn, run q -> 4 consecutive weight rows
+  float4 bs[2][4];
+#pragma unroll
+  for (int tn = 0; tn < 2; ++tn) {
+    const int wrow0 = weight_row<kGemm1>(g, unit, kStreamUnit, tn * 32);  // first weight row of the tile
+    const float* src = g.b_scale + static_cast<int64_t>(e) * g.n + wrow0 + hk * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bs[tn][q] = *reinterpret_cast<const float4*>(src + q * 8);
+  }
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int r = tm * 32 + rl;
+    const float xs = r < mrows ? row_scale<kGather>(g, rs, row0 + r) : 0.0f;
+    const int rkey = (r >> 1) & 7;
+#pragma unroll
+    for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 ws = bs[tn][q];
+        const uint32_t lo = pack_bf16x2(acc[tm][tn][4 * q] * xs * ws.x, acc[tm][tn][4 * q + 1] * xs * ws.y);
+        const uint32_t hi = pack_bf16x2(acc[tm][tn][4 * q + 2] * xs * ws.z, acc[tm][tn][4 * q + 3] * xs * ws.w);
+        // columns tn*32 + 8q + 4hk .. +4 -> bytes 64tn + 16q + 8hk: piece 4tn + q, half hk
+        const int piece = (4 * tn + q) ^ rkey;
+        *reinterpret_cast<uint2*>(wlds + r * 128 + piece * 16 + hk * 8) = make_uint2(lo, hi);
+      }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's LDS writes before its reads
+  const int piece = lane & 7;
+  // GEMM1: pieces 0-3 are gate channels unit*32 + 8p, pieces 4-7 the up channels
+  const int64_t ld = kGemm1 ? 2 * static_cast<int64_t>(g.sw.inter) : g.n;
+  const int col = kGemm1 ? (piece < 4 ? unit * 32 + piece * 8 : g.sw.inter + unit * 32 + (piece - 4) * 8)
+                         : unit * 64 + piece * 8;
+  uint16_t* out = (kGemm1 ? reinterpret_cast<uint16_t*>(g.sw.y) : g.c) + static_cast<int64_t>(row0) * ld + col;
+#pragma unroll 8
+  for (int i = 0; i < kTileBM / 8; ++i) {
+    const int rr = i * 8 + (lane >> 3);
+    const int4 val = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
+    if (rr < mrows) *reinterpret_cast<int4*>(out + rr * ld) = val;
+  }
+}
+
+template <bool kGather, bool kSwiglu>
+__device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
+                          uint8_t* smem) {
+  constexpr int TM = kTileBM / 32, TN = kStreamUnit / 32;     // 8 x 2
+  constexpr int kALoads = kTileBM * kWideBK / 16 / kWideThreads;  // 8
+  constexpr int kRowsPerLoad = kWideThreads / (kWideBK / 16);     // 32
+  const int tid = opaque_tid();
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int stages = g.k / kWideBK;
+  const int steps = stages * (kWideBK / 64);
+  const int units = g.n / kStreamUnit;
+  const int unit_raw = nb * kWideWaves + wave;
+  const bool active = unit_raw < units;
+  const int unit = active ? unit_raw : units - 1;  // a partial column block: any valid columns
+  const int hk = lane >> 5;
+
+  // A: load i covers row i*32 + tid/8, piece tid % 8
+  const uint8_t* a_src[kALoads];
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) {
+    const int r = i * kRowsPerLoad + (tid >> 3);
+    a_src[i] = a_row_ptr<kGather>(g, rs, row0 + (r < mrows ? r : 0)) + (tid & 7) * 16;
+  }
+  const int a_dst0 = (tid >> 3) * kWideBK + (((tid & 7) ^ ((tid >> 4) & 7)) << 4);
+  // two register sets: a stage's A is loaded one stage before it is written to LDS, which is
+  // one stage before it is read
+  int4 ra[2][kALoads];
+  auto load_a = [&](int set, int i, int kt) { ra[set][i] = ld16(a_src[i] + kt * kWideBK); };
+  auto store_a = [&](int set, int i, int kt) {
+    *reinterpret_cast<int4*>(smem + (kt % kWideBufs) * kWideStage + a_dst0 + i * kRowsPerLoad * kWideBK) =
+        ra[set][i];
+  };
+  // B: column tile tn of the wave's unit; 64-k step s of the lane's column at + s*1024 (+256)
+  const uint8_t* bp[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int n = weight_row<kSwiglu>(g, unit, kStreamUnit, tn * 32 + (lane & 31));
+    bp[tn] = g.b + (static_cast<int64_t>(e) * (g.n / 16) + (n >> 4)) * (static_cast<int64_t>(g.k) * 16) +
+             (n & 15) * 16 + hk * 512;
+  }
+  int4 br[kWideRing][TN][2];
+  auto load_b = [&](int slot, int s) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const uint8_t* q = bp[tn] + static_cast<int64_t>(s) * 1024;
+      br[slot][tn][0] = ld16(q);
+      br[slot][tn][1] = ld16(q + 256);
+    }
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int rkey = ((lane & 31) >> 1) & 7;
+  auto read_a = [&](int kt, int ks, int tm) {
+    const int p0 = ks * 4 + hk * 2;
+    const uint8_t* ar = smem + (kt % kWideBufs) * kWideStage + (tm * 32 + (lane & 31)) * kWideBK;
+    return make_v8i(*reinterpret_cast<const int4*>(ar + ((p0 ^ rkey) << 4)),
+                    *reinterpret_cast<const int4*>(ar + (((p0 + 1) ^ rkey) << 4)));
+  };
+  // A stage = 16 MFMA groups (2 steps x 8 row tiles, 2 MFMAs each). The A operand of group
+  // g + 3 is read while group g's MFMAs run (ring of 4 operands; the last groups read the next
+  // stage's first operands, whose buffer is complete since the previous barrier), which
+  // covers the LDS latency with one wave per SIMD. Order pinned by sched_barrier.
+  constexpr int kGroups = (kWideBK / 64) * TM;
+  constexpr int kAhead = 3;
+  static_assert(kGroups % (kAhead + 1) == 0, "operand ring index must repeat per stage");
+  v8i abuf[kAhead + 1];
+  auto read_group = [&](int kt, int gi) {
+    const int g2 = gi % kGroups;
+    return read_a(kt + gi / kGroups, g2 / TM, g2 % TM);
+  };
+  const int last_step = steps - 1;
+  const int last_stage = stages - 1;
+  // stage kt: 16 groups; groups 0-7 each load one piece of stage kt + 3's A into register set
+  // `lset`, groups 8-15 each write one piece of stage kt + 2's A (set `wset`, loaded during
+  // the previous stage) into its LDS buffer, each step's last group refills its B ring slot
+  // with the step 4 ahead; then the barrier. Spread out, these loads and LDS writes issue in
+  // the gaps between MFMAs instead of stalling the MFMA pipe in bursts.
+  auto stage = [&](int kt, int slot0, int wset, int lset) {
+    const int kt_load = min(kt + 3, last_stage);
+#pragma unroll
+    for (int gi = 0; gi < kGroups; ++gi) {
+      const int ks = gi / TM, tm = gi % TM;
+      abuf[(gi + kAhead) % (kAhead + 1)] = read_group(kt, gi + kAhead);
+      if (gi < kALoads) load_a(lset, gi, kt_load);
+      else store_a(wset, gi - kALoads, kt + 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        acc[tm][tn] = mfma_fp8(make_v8i(br[slot0 + ks][tn][0], br[slot0 + ks][tn][1]),
+                               abuf[gi % (kAhead + 1)], acc[tm][tn]);  // transposed tile
+      __builtin_amdgcn_sched_barrier(0);
+      if (tm == TM - 1) {
+        load_b(slot0 + ks, min(kt * (kWideBK / 64) + ks + kWideRing, last_step));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    lds_barrier();
+  };
+  static_assert(kGroups == 2 * kALoads, "one A load and one A write per group");
+
+  // prologue: A stages 0 and 1 into LDS, stage 2 into register set 0, B steps 0..3, the first
+  // operands
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) load_a(0, i, 0);
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) load_a(1, i, min(1, last_stage));
+#pragma unroll
+  for (int sl = 0; sl < kWideRing; ++sl) load_b(sl, min(sl, last_step));
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) store_a(0, i, 0);
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) load_a(0, i, min(2, last_stage));
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) store_a(1, i, 1);
+  lds_barrier();
+#pragma unroll
+  for (int gi = 0; gi < kAhead; ++gi) abuf[gi] = read_group(0, gi);
+  // two stages per iteration, so that the ring slots are compile-time indices; every load is
+  // issued unconditionally (past the end it reloads the last step or stage), which keeps the
+  // compiler's load counting exact
+  for (int kt = 0; kt < stages; kt += 2) {  // stages is even (k % 256 == 0)
+    stage(kt, 0, 0, 1);
+    stage(kt + 1, 2, 1, 0);
+  }
+  // every wave has passed its last LDS read of A (the barrier that ended the last stage)
+  if (!active) return;
+  store_wide<kGather, kSwiglu>(g, rs, acc, e, row0, mrows, unit, smem + wave * kWideOut);
+}
+
 // ------------------------------------------------------------------ in-kernel routing
 // For small task counts GEMM1 routes the tokens itself instead of a separate routing kernel:
 // every workgroup counts all tasks with its 8 waves (LDS atomics into per-wave counts; integer
@@ -578,7 +788,8 @@ __device__ __forceinline__ int stream_blocks(const GemmArgs& g) {
 // experts and s_tile[e] with the expert's engine (1 = TILE), from the routed rows s_count[e].
 // A STREAM item is one (64-row chunk, 512-column block); a TILE item is one 256 x 256 tile
 // (row-block major).
-__device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const int* s_count) {
+__device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const int* s_count,
+                           bool all_tile = false) {
   const int E = g.num_experts;
   const int lane = lane_id();
   const int stream_nb = stream_blocks(g);
@@ -590,7 +801,7 @@ __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const 
       int items = 0;
       if (e < E) {
         const int cnt = s_count[e];
-        const bool tile = g.engine == GemmEngine::kTile ||
+        const bool tile = all_tile || g.engine == GemmEngine::kTile ||
                           (g.engine == GemmEngine::kAuto && cnt > kStreamRows);
         items = tile ? (cnt + kTileBM - 1) / kTileBM * tile_nb
                      : (cnt + kStreamRows - 1) / kStreamRows * stream_nb;
@@ -616,6 +827,18 @@ __device__ __forceinline__ int expert_of_item(const int* s_prefix, int E, int t)
     if (s_prefix[mid] <= t) lo = mid; else hi = mid;
   }
   return lo;
+}
+
+// TILE item `local` of an expert with cnt rows -> (row block mt, column block nb): row blocks
+// in groups of 4, columns inside a group, so that the consecutive items an XCD runs together
+// form 4 x 8 tiles sharing A rows and B columns in its L2.
+__device__ __forceinline__ void tile_coords(int local, int cnt, int tile_nb, int& mt, int& nb) {
+  const int mblocks = (cnt + kTileBM - 1) / kTileBM;
+  const int group = local / (4 * tile_nb);
+  const int in_group = local - group * 4 * tile_nb;
+  const int rows_in_group = min(4, mblocks - group * 4);
+  nb = in_group / rows_in_group;
+  mt = group * 4 + (in_group - nb * rows_in_group);
 }
 
 template <bool kGather, bool kSwiglu>
@@ -705,14 +928,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
     const int cnt = s_count[e];
     const int off_e = s_off[e];
     if (s_tile[e]) {
-      // row blocks in groups of 4, columns inside a group, so that the consecutive items an
-      // XCD runs together form 4 x 8 tiles sharing A rows and B columns in its L2
-      const int mblocks = (cnt + kTileBM - 1) / kTileBM;
-      const int group = local / (4 * tile_nb);
-      const int in_group = local - group * 4 * tile_nb;
-      const int rows_in_group = min(4, mblocks - group * 4);
-      const int nb = in_group / rows_in_group;
-      const int mt = group * 4 + (in_group - nb * rows_in_group);
+      int mt, nb;
+      tile_coords(local, cnt, tile_nb, mt, nb);
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
         const int r0 = mt * kTileBM;
@@ -746,6 +963,63 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   }
 }
 
+// Persistent dispatcher of the WIDE engine: every expert's rows as 256 x 256 tiles, items dealt
+// to the XCDs in contiguous ranges like the 8-wave dispatcher's.
+template <bool kGather, bool kSwiglu>
+__global__ __launch_bounds__(kWideThreads, 1) void wide_gemm_kernel(GemmArgs g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_prefix[kMaxGemmExperts + 1];
+  __shared__ int s_tile[kMaxGemmExperts];
+  __shared__ int s_count[kMaxGemmExperts];
+  __shared__ int s_off[kMaxGemmExperts + 1];
+  const int E = g.num_experts;
+  for (int e = threadIdx.x; e <= E; e += kWideThreads) {
+    if (e < E) s_count[e] = g.counts[e];
+    s_off[e] = g.offsets[e];
+  }
+  __syncthreads();
+  plan_items(g, s_prefix, s_tile, s_count, true);
+  __syncthreads();
+  const int total = s_prefix[E];
+  const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
+  const int nwg = gridDim.x;
+  const bool by_xcd = nwg % 8 == 0;
+  const int xcd = blockIdx.x % 8;
+  const int first = by_xcd ? static_cast<int>(static_cast<int64_t>(total) * xcd / 8) + blockIdx.x / 8
+                           : static_cast<int>(blockIdx.x);
+  const int last = by_xcd ? static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8) : total;
+  const int step = by_xcd ? nwg / 8 : nwg;
+  const RowSrc rs{g.row_token, g.sw.row_weight, 0};
+  for (int t = first; t < last; t += step) {
+    const int e = expert_of_item(s_prefix, E, t);
+    const int cnt = s_count[e];
+    int mt, nb;
+    tile_coords(t - s_prefix[e], cnt, tile_nb, mt, nb);
+    wide_tile<kGather, kSwiglu>(g, rs, e, s_off[e] + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM), nb,
+                                smem);
+    __syncthreads();
+  }
+}
+
+template <bool kGather, bool kSwiglu>
+hipError_t launch_wide(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
+  static bool attr_set = false;  // the 96 KB of dynamic LDS exceeds the default limit
+  if (!attr_set) {
+    const hipError_t err =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_gemm_kernel<kGather, kSwiglu>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kWideSmemBytes);
+    if (err != hipSuccess) return err;
+    attr_set = true;
+  }
+  const int64_t bound =
+      (static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * ((g.n + kTileBN - 1) / kTileBN);
+  int64_t grid = num_cus;  // one 4-wave workgroup per CU
+  if (grid > bound) grid = bound;
+  hipLaunchKernelGGL((wide_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kWideThreads), kWideSmemBytes, stream, g);
+  return hipGetLastError();
+}
+
 template <bool kGather, bool kSwiglu>
 hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
   static bool attr_set = false;  // the 128 KB of dynamic LDS exceeds the default limit
@@ -776,6 +1050,15 @@ hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStrea
 int gemm_route_max_tasks() { return kFusedMaxTasks; }
 int gemm_route_max_experts() { return kFusedMaxExperts; }
 
+// Many rows per expert on average: every expert as WIDE tiles (one launch, no per-expert engine
+// choice). More tasks than the in-kernel routing takes, so the two never meet; the choice
+// depends only on the shape and the row bound, so separate stage calls agree on it.
+bool gemm_wide_selected(const GemmArgs& g, int max_rows) {
+  return g.engine != GemmEngine::kStream && g.k % (2 * kWideBK) == 0 && g.n % kStreamUnit == 0 &&
+         max_rows > kFusedMaxTasks &&
+         static_cast<int64_t>(max_rows) >= static_cast<int64_t>(kWideMinRowsPerExpert) * g.num_experts;
+}
+
 bool gemm_shape_supported(int n, int k) {
   return n > 0 && k > 0 && n % 128 == 0 && k % 128 == 0;
 }
@@ -783,12 +1066,16 @@ bool gemm_shape_supported(int n, int k) {
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
   if (max_rows <= 0) return hipSuccess;
   if (g.num_experts > kMaxGemmExperts) return hipErrorInvalidValue;
+  const bool wide = gemm_wide_selected(g, max_rows);
+  if (wide && g.route_in_kernel) return hipErrorInvalidValue;
   if (g.sw.enabled) {
     if (g.row_token == nullptr || g.n != 2 * g.sw.inter) return hipErrorInvalidValue;
-    return launch_engines<true, true>(g, max_rows, num_cus, stream);
+    return wide ? launch_wide<true, true>(g, max_rows, num_cus, stream)
+                : launch_engines<true, true>(g, max_rows, num_cus, stream);
   }
   if (g.row_token != nullptr) return hipErrorInvalidValue;
-  return launch_engines<false, false>(g, max_rows, num_cus, stream);
+  return wide ? launch_wide<false, false>(g, max_rows, num_cus, stream)
+              : launch_engines<false, false>(g, max_rows, num_cus, stream);
 }
 
 }  // namespace mmoe

@@ -44,7 +44,8 @@ struct SwigluEpilogue {
   int enabled;
   int inter;                // I: gate weight rows [0, I), up rows [I, 2I)
   const float* row_weight;  // [rows] top-k weight of each routed row
-  float* y;                 // f32 [rows, I] SwiGLU output (before requant)
+  float* y;                 // f32 [rows, I] SwiGLU output (before requant), or with the WIDE
+                            // kernel bf16 [rows, 2I] pre-activation h (gemm_wide_selected)
   int has_clamp;
   float clamp;
 };
@@ -73,15 +74,20 @@ struct GemmArgs {
 // device from counts (max_rows bounds the grid only).
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream);
 bool gemm_shape_supported(int n, int k);
+// True when launch_grouped_gemm runs the WIDE kernel for g: GEMM1 then writes the bf16
+// pre-activation h [rows, 2I] instead of the SwiGLU output y (requant computes the SwiGLU).
+bool gemm_wide_selected(const GemmArgs& g, int max_rows);
 // Largest task count (S*K) and expert count GEMM1 can route in-kernel.
 int gemm_route_max_tasks();
 int gemm_route_max_experts();
 
 // Per-row requant of the SwiGLU output: amax = max |y| (written out), a = max(amax, 1e-4);
-// act = e4m3(clip(y * 448/a)); act_scale = a/448 -- for rows < meta[0].
-hipError_t launch_requant(const float* y, float* amax, const int32_t* meta,
-                          uint8_t* act, float* act_scale, int64_t max_rows, int inter,
-                          int num_cus, hipStream_t stream);
+// act = e4m3(clip(y * 448/a)); act_scale = a/448 -- for rows < meta[0]. y is GEMM1's fp32
+// SwiGLU output, or with from_h the SwiGLU of GEMM1's bf16 pre-activation h [rows, 2I]
+// computed here (sw: route weights and clamp). meta[1] records which (1 = from h).
+hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw, float* amax,
+                          int32_t* meta, uint8_t* act, float* act_scale, int64_t max_rows,
+                          int inter, int num_cus, hipStream_t stream);
 
 struct CombineArgs {
   uint16_t* y;                     // bf16 [S, H]

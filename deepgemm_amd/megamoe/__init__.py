@@ -275,7 +275,9 @@ class SymmBuffer:
     def scratch_view(self, name: str, num_rows: Optional[int] = None) -> torch.Tensor:
         """Intermediate tensors of the last call: counts, offsets, meta, output_index,
         row_token, row_weight, m_indices, act_scale, amax (max |y| per row), y (SwiGLU x
-        weight, f32), act (requantised y), part (GEMM2 rows)."""
+        weight, f32), act (requantised y), part (GEMM2 rows). When meta[1] == 1 the GEMM1 of
+        the call left the bf16 pre-activation instead of y, in the same bytes: view it as h
+        ([rows, 2I], gate channels then up channels)."""
         l = self.scratch_layout
         e, t, k = self.num_experts, self.num_max_tokens_per_rank, self.num_topk
         rows = int(l.row_capacity if num_rows is None else num_rows)
@@ -290,6 +292,7 @@ class SymmBuffer:
             "act_scale": (l.act_scale_offset, torch.float32, (rows,)),
             "amax": (l.amax_offset, torch.float32, (rows,)),
             "y": (l.y_offset, torch.float32, (rows, self.intermediate_hidden)),
+            "h": (l.y_offset, torch.bfloat16, (rows, 2 * self.intermediate_hidden)),
             "act": (l.act_offset, torch.float8_e4m3fn, (rows, self.intermediate_hidden)),
             "part": (l.part_offset, torch.bfloat16, (rows, self.hidden)),
         }
