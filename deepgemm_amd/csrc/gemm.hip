@@ -487,8 +487,10 @@ constexpr int kWideBK = 128;
 constexpr int kWideStage = kTileBM * kWideBK;  // 32 KB of A
 constexpr int kWideBufs = 3;
 constexpr int kWideOut = kTileBM * 128;  // a wave's staged output tile (256 rows x 128 bytes)
-constexpr int kWideSmemBytes = kWideWaves * kWideOut > kWideBufs * kWideStage ? kWideWaves * kWideOut
-                                                                                 : kWideBufs * kWideStage;
+constexpr int kWideTables = kWideWaves * kWideOut > kWideBufs * kWideStage ? kWideWaves * kWideOut
+                                                                               : kWideBufs * kWideStage;
+// after the A ring / output staging: the tile's 256 row scales, then its 256 weight-row scales
+constexpr int kWideSmemBytes = kWideTables + 2 * kTileBM * 4;
 constexpr int kWideRing = 4;  // 64-k steps of B in registers
 constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that select it
 
@@ -503,25 +505,28 @@ constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that sele
 // gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
 // bf16 partials.
 template <bool kGather, bool kGemm1>
-__device__ __forceinline__ void store_wide(const GemmArgs& g, const RowSrc& rs,
-                                           const v16f (&acc)[kTileBM / 32][2], int e, int row0,
-                                           int mrows, int unit, uint8_t* wlds) {
+__device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[kTileBM / 32][2],
+                                           int row0, int mrows, int unit, uint8_t* wlds,
+                                           const uint8_t* tables) {
   constexpr int TM = kTileBM / 32;
   const int lane = opaque_tid() & (kWave - 1);
   const int rl = lane & 31, hk = lane >> 5;
-  // column scales: tile tn, run q -> 4 consecutive weight rows
+  // column scales (tile tn, run q: 4 consecutive weight rows) and row scales from the tables
+  // the prologue filled
+  const float* s_xs = reinterpret_cast<const float*>(tables);
+  const float* s_bs = s_xs + kTileBM + (opaque_tid() / kWave) * kStreamUnit;
   float4 bs[2][4];
 #pragma unroll
-  for (int tn = 0; tn < 2; ++tn) {
-    const int wrow0 = weight_row<kGemm1>(g, unit, kStreamUnit, tn * 32);  // first weight row of the tile
-    const float* src = g.b_scale + static_cast<int64_t>(e) * g.n + wrow0 + hk * 4;
+  for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) bs[tn][q] = *reinterpret_cast<const float4*>(src + q * 8);
-  }
+    for (int q = 0; q < 4; ++q) bs[tn][q] = *reinterpret_cast<const float4*>(s_bs + tn * 32 + q * 8 + hk * 4);
+  float xs_row[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) xs_row[tm] = s_xs[tm * 32 + rl];
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) {
     const int r = tm * 32 + rl;
-    const float xs = r < mrows ? row_scale<kGather>(g, rs, row0 + r) : 0.0f;
+    const float xs = xs_row[tm];
     const int rkey = (r >> 1) & 7;
 #pragma unroll
     for (int tn = 0; tn < 2; ++tn)
@@ -658,8 +663,11 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   };
   static_assert(kGroups == 2 * kALoads, "one A load and one A write per group");
 
-  // prologue: A stages 0 and 1 into LDS, stage 2 into register set 0, B steps 0..3, the first
-  // operands
+  // prologue: the epilogue's scales (thread t: row t's A scale, and the weight-row scale of
+  // its wave's column lane), A stages 0 and 1 into LDS, stage 2 into register set 0, B steps
+  // 0..3, the first operands. Rows past mrows take the last row's scale (never stored).
+  const float pre_xs = row_scale<kGather>(g, rs, row0 + min(tid, mrows - 1));
+  const float pre_bs = g.b_scale[static_cast<int64_t>(e) * g.n + weight_row<kSwiglu>(g, unit, kStreamUnit, lane)];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) load_a(0, i, 0);
 #pragma unroll
@@ -672,6 +680,8 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   for (int i = 0; i < kALoads; ++i) load_a(0, i, min(2, last_stage));
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) store_a(1, i, 1);
+  reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
+  reinterpret_cast<float*>(smem + kWideTables)[kTileBM + tid] = pre_bs;
   lds_barrier();
 #pragma unroll
   for (int gi = 0; gi < kAhead; ++gi) abuf[gi] = read_group(0, gi);
@@ -684,7 +694,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   }
   // every wave has passed its last LDS read of A (the barrier that ended the last stage)
   if (!active) return;
-  store_wide<kGather, kSwiglu>(g, rs, acc, e, row0, mrows, unit, smem + wave * kWideOut);
+  store_wide<kGather, kSwiglu>(g, acc, row0, mrows, unit, smem + wave * kWideOut, smem + kWideTables);
 }
 
 // ------------------------------------------------------------------ in-kernel routing
