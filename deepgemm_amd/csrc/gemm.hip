@@ -720,7 +720,7 @@ __device__ __forceinline__ int fused_per_wave(int ntasks) {
 // Per-wave counts of all tasks into s_wcnt[wave][e] and each task's expert into s_ev;
 // workgroup 0 also marks the invalid tasks.
 __device__ void fused_count(const RouteArgs& a, int ntasks, int (*s_wcnt)[kMaxGemmExperts],
-                            uint8_t* s_ev, bool publisher) {
+                            uint8_t* s_ev, float* s_task_w, bool publisher) {
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int per = fused_per_wave(ntasks);
@@ -735,6 +735,7 @@ __device__ void fused_count(const RouteArgs& a, int ntasks, int (*s_wcnt)[kMaxGe
       const int task = b + p * kWave + lane;
       if (task < end) {
         s_ev[task] = ev[p] < 0 ? 255 : static_cast<uint8_t>(ev[p]);
+        s_task_w[task] = wv[p];
         if (ev[p] >= 0) atomicAdd(&s_wcnt[wave][ev[p]], 1);
         else if (publisher) a.output_index[task] = -1;
       }
@@ -746,9 +747,9 @@ __device__ void fused_count(const RouteArgs& a, int ntasks, int (*s_wcnt)[kMaxGe
 // row table; rows in [w_lo0, w_hi0) or [w_lo1, w_hi1) are this workgroup's to write out.
 // Ends with the table complete (workgroup barrier).
 __device__ void fused_rows(const RouteArgs& a, int ntasks, int e, int cnt, int off_e,
-                           const int (*s_wcnt)[kMaxGemmExperts], const uint8_t* s_ev, int r_lo,
-                           int w_lo0, int w_hi0, int w_lo1, int w_hi1, int* s_task, int* s_tok,
-                           float* s_rw) {
+                           const int (*s_wcnt)[kMaxGemmExperts], const uint8_t* s_ev,
+                           const float* s_task_w, int r_lo, int w_lo0, int w_hi0, int w_lo1,
+                           int w_hi1, int* s_task, int* s_tok, float* s_rw) {
   const int lane = lane_id();
   const int wave = static_cast<int>(threadIdx.x) / kWave;
   const int per = fused_per_wave(ntasks);
@@ -772,7 +773,7 @@ __device__ void fused_rows(const RouteArgs& a, int ntasks, int e, int cnt, int o
   const int n = min(kRowTable, cnt - r_lo);
   for (int t = static_cast<int>(threadIdx.x); t < n; t += kGemmThreads) {
     const int task = s_task[t];
-    const float w = a.topk_w[task];
+    const float w = s_task_w != nullptr ? s_task_w[task] : a.topk_w[task];
     s_rw[t] = w;
     const int rank = r_lo + t;
     if ((rank >= w_lo0 && rank < w_hi0) || (rank >= w_lo1 && rank < w_hi1)) {
@@ -830,13 +831,17 @@ __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const 
   }
 }
 
+// The expert owning item t: the last e with s_prefix[e] <= t (s_prefix is non-decreasing, so
+// that is the count of such e, minus one). One LDS read and one ballot per 64 experts, the
+// whole wave at once, instead of a chain of dependent reads.
 __device__ __forceinline__ int expert_of_item(const int* s_prefix, int E, int t) {
-  int lo = 0, hi = E;  // last e with s_prefix[e] <= t
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (s_prefix[mid] <= t) lo = mid; else hi = mid;
+  const int lane = lane_id();
+  int below = 0;
+  for (int e0 = 0; e0 < E; e0 += kWave) {
+    const int e = e0 + lane;
+    below += __popcll(__ballot(e < E && s_prefix[e] <= t));
   }
-  return lo;
+  return below - 1;
 }
 
 // TILE item `local` of an expert with cnt rows -> (row block mt, column block nb): row blocks
@@ -851,7 +856,10 @@ __device__ __forceinline__ void tile_coords(int local, int cnt, int tile_nb, int
   mt = group * 4 + (in_group - nb * rows_in_group);
 }
 
-template <bool kGather, bool kSwiglu>
+// kAnyK: K not a multiple of the STREAM chunk (small shapes); the production shapes compile
+// without those variants, which keeps the kernel's code (and its cold instruction fetches in
+// the one-time prologue) smaller.
+template <bool kGather, bool kSwiglu, bool kAnyK>
 __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_prefix[kMaxGemmExperts + 1];
@@ -869,36 +877,40 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   int ntasks = 0;
   if (fused) {
     ntasks = effective_tokens(ra.runtime_tokens, ra.host_tokens) * ra.topk;
-    for (int i = threadIdx.x; i < kGemmWaves * E; i += kGemmThreads) s_wcnt[i / E][i % E] = 0;
-    __syncthreads();
-    fused_count(ra, ntasks, s_wcnt, s_ev, blockIdx.x == 0);
-    __syncthreads();
-    for (int e = threadIdx.x; e < E; e += kGemmThreads) {  // per-wave counts -> bases, totals
-      int run = 0;
-      for (int w = 0; w < kGemmWaves; ++w) {
-        const int c = s_wcnt[w][e];
-        s_wcnt[w][e] = run;
-        run += c;
-      }
-      s_count[e] = run;
+    {  // each wave clears its own count row: only that wave adds to it, so no barrier is needed
+      const int wave = static_cast<int>(threadIdx.x) / kWave;
+      for (int e = lane_id(); e < E; e += kWave) s_wcnt[wave][e] = 0;
     }
+    // the route weights stay in the (still unused) dynamic LDS for the first item's row table
+    fused_count(ra, ntasks, s_wcnt, s_ev, reinterpret_cast<float*>(smem), blockIdx.x == 0);
     __syncthreads();
-    if (threadIdx.x < kWave) {  // expert offsets: exclusive scan of the counts
+    if (threadIdx.x < kWave) {
+      // wave 0: per-wave counts -> per-wave bases and expert totals, the exclusive scan of the
+      // totals (expert offsets), then the work plan; LDS traffic of one wave stays in order
       const int lane = lane_id();
       int carry = 0;
       for (int e0 = 0; e0 < E; e0 += kWave) {
         const int e = e0 + lane;
-        const int c = e < E ? s_count[e] : 0;
-        int inc = c;
+        int run = 0;
+        if (e < E) {
+          for (int w = 0; w < kGemmWaves; ++w) {
+            const int c = s_wcnt[w][e];
+            s_wcnt[w][e] = run;
+            run += c;
+          }
+          s_count[e] = run;
+        }
+        int inc = run;
 #pragma unroll
         for (int off = 1; off < kWave; off <<= 1) {
           const int u = __shfl_up(inc, off, kWave);
           if (lane >= off) inc += u;
         }
-        if (e < E) s_off[e] = carry + inc - c;
+        if (e < E) s_off[e] = carry + inc - run;
         carry += __shfl(inc, kWave - 1, kWave);
       }
       if (lane == 0) s_off[E] = carry;
+      plan_items(g, s_prefix, s_tile, s_count);
     }
     __syncthreads();
     if (blockIdx.x == 0) {  // the routing kernel's outputs that the later stages read
@@ -915,14 +927,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
       s_off[e] = g.offsets[e];
     }
     __syncthreads();
+    plan_items(g, s_prefix, s_tile, s_count);
+    __syncthreads();
   }
-  plan_items(g, s_prefix, s_tile, s_count);
-  __syncthreads();
   const int total = s_prefix[E];
   const int stream_nb = stream_blocks(g);
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
-  const bool fast1 = g.k % (kAChunk / 32) == 0;
-  const bool fast2 = g.k % (kAChunk / 64) == 0;
+  const bool fast1 = !kAnyK || g.k % (kAChunk / 32) == 0;
+  const bool fast2 = !kAnyK || g.k % (kAChunk / 64) == 0;
   // Items are dealt to the XCDs in contiguous ranges (workgroup b runs on XCD b % 8), so the
   // workgroups of an XCD share its L2 for the same experts' A rows.
   const int nwg = gridDim.x;
@@ -932,6 +944,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
                            : static_cast<int>(blockIdx.x);
   const int last = by_xcd ? static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8) : total;
   const int step = by_xcd ? nwg / 8 : nwg;
+  const float* task_w = reinterpret_cast<const float*>(smem);  // valid until the first item's loads
   for (int t = first; t < last; t += step) {
     const int e = expert_of_item(s_prefix, E, t);
     const int local = t - s_prefix[e];
@@ -943,8 +956,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
         const int r0 = mt * kTileBM;
-        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, r0, nb == 0 ? r0 : 0,
-                   nb == 0 ? r0 + kTileBM : 0, 0, 0, s_task, s_tok, s_rw);
+        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, t == first ? task_w : nullptr, r0,
+                   nb == 0 ? r0 : 0, nb == 0 ? r0 + kTileBM : 0, 0, 0, s_task, s_tok, s_rw);
         rs = RowSrc{s_tok, s_rw, off_e + r0};
       }
       tile_tile<kGather, kSwiglu>(g, rs, e, off_e + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM),
@@ -957,16 +970,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
         const int r0 = mc * kStreamRows;
-        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, r0, nb == 0 ? r0 : 0,
-                   nb == 0 ? r0 + kStreamRows : 0, 0, 0, s_task, s_tok, s_rw);
+        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, t == first ? task_w : nullptr, r0,
+                   nb == 0 ? r0 : 0, nb == 0 ? r0 + kStreamRows : 0, 0, 0, s_task, s_tok, s_rw);
         rs = RowSrc{s_tok, s_rw, row0};
       }
       if (mrows > 32) {
         if (fast2) stream_tile<kGather, kSwiglu, 2, true>(g, rs, e, row0, mrows, nb, smem);
-        else stream_tile<kGather, kSwiglu, 2, false>(g, rs, e, row0, mrows, nb, smem);
+        else if (kAnyK) stream_tile<kGather, kSwiglu, 2, false>(g, rs, e, row0, mrows, nb, smem);
       } else {
         if (fast1) stream_tile<kGather, kSwiglu, 1, true>(g, rs, e, row0, mrows, nb, smem);
-        else stream_tile<kGather, kSwiglu, 1, false>(g, rs, e, row0, mrows, nb, smem);
+        else if (kAnyK) stream_tile<kGather, kSwiglu, 1, false>(g, rs, e, row0, mrows, nb, smem);
       }
     }
     __syncthreads();
@@ -1030,12 +1043,12 @@ hipError_t launch_wide(const GemmArgs& g, int max_rows, int num_cus, hipStream_t
   return hipGetLastError();
 }
 
-template <bool kGather, bool kSwiglu>
-hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
+template <bool kGather, bool kSwiglu, bool kAnyK>
+hipError_t launch_engines_k(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
   static bool attr_set = false;  // the 128 KB of dynamic LDS exceeds the default limit
   if (!attr_set) {
     const hipError_t err =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<kGather, kSwiglu>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<kGather, kSwiglu, kAnyK>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes);
     if (err != hipSuccess) return err;
     attr_set = true;
@@ -1050,9 +1063,15 @@ hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStrea
                                                         : std::max(stream_items, tile_items);
   int64_t grid = num_cus;  // one 8-wave workgroup per CU
   if (grid > bound) grid = bound;
-  hipLaunchKernelGGL((grouped_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
+  hipLaunchKernelGGL((grouped_gemm_kernel<kGather, kSwiglu, kAnyK>), dim3(static_cast<unsigned>(grid)),
                      dim3(kGemmThreads), kSmemBytes, stream, g);
   return hipGetLastError();
+}
+
+template <bool kGather, bool kSwiglu>
+hipError_t launch_engines(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
+  return g.k % (kAChunk / 32) == 0 ? launch_engines_k<kGather, kSwiglu, false>(g, max_rows, num_cus, stream)
+                                    : launch_engines_k<kGather, kSwiglu, true>(g, max_rows, num_cus, stream);
 }
 
 }  // namespace
