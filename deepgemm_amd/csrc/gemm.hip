@@ -504,11 +504,10 @@ constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that sele
 // GEMM1 (kGemm1) writes the pre-activation h = bf16(acc * x_scale * w_scale) [rows, 2I] with
 // gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
 // bf16 partials.
-template <bool kGather, bool kGemm1>
-__device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[kTileBM / 32][2],
-                                           int row0, int mrows, int unit, uint8_t* wlds,
+template <bool kGather, bool kGemm1, int TM>
+__device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[TM][2], int row0,
+                                           int mrows, int unit, uint8_t* wlds,
                                            const uint8_t* tables) {
-  constexpr int TM = kTileBM / 32;
   const int lane = opaque_tid() & (kWave - 1);
   const int rl = lane & 31, hk = lane >> 5;
   // column scales (tile tn, run q: 4 consecutive weight rows) and row scales from the tables
@@ -548,18 +547,20 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
                          : unit * 64 + piece * 8;
   uint16_t* out = (kGemm1 ? reinterpret_cast<uint16_t*>(g.sw.y) : g.c) + static_cast<int64_t>(row0) * ld + col;
 #pragma unroll 8
-  for (int i = 0; i < kTileBM / 8; ++i) {
+  for (int i = 0; i < TM * 4; ++i) {
     const int rr = i * 8 + (lane >> 3);
     const int4 val = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
     if (rr < mrows) *reinterpret_cast<int4*>(out + rr * ld) = val;
   }
 }
 
-template <bool kGather, bool kSwiglu>
+// TM row tiles of 32: 8 for a full tile, 4 for an expert's last tile of at most 128 rows (half
+// the MFMAs and A traffic for the row remainder).
+template <bool kGather, bool kSwiglu, int TM>
 __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
                           uint8_t* smem) {
-  constexpr int TM = kTileBM / 32, TN = kStreamUnit / 32;     // 8 x 2
-  constexpr int kALoads = kTileBM * kWideBK / 16 / kWideThreads;  // 8
+  constexpr int TN = kStreamUnit / 32;                        // 2
+  constexpr int kALoads = TM * 32 * kWideBK / 16 / kWideThreads;  // TM
   constexpr int kRowsPerLoad = kWideThreads / (kWideBK / 16);     // 32
   const int tid = opaque_tid();
   const int lane = tid & (kWave - 1);
@@ -694,7 +695,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   }
   // every wave has passed its last LDS read of A (the barrier that ended the last stage)
   if (!active) return;
-  store_wide<kGather, kSwiglu>(g, acc, row0, mrows, unit, smem + wave * kWideOut, smem + kWideTables);
+  store_wide<kGather, kSwiglu, TM>(g, acc, row0, mrows, unit, smem + wave * kWideOut, smem + kWideTables);
 }
 
 // ------------------------------------------------------------------ in-kernel routing
@@ -1018,8 +1019,11 @@ __global__ __launch_bounds__(kWideThreads, 1) void wide_gemm_kernel(GemmArgs g) 
     const int cnt = s_count[e];
     int mt, nb;
     tile_coords(t - s_prefix[e], cnt, tile_nb, mt, nb);
-    wide_tile<kGather, kSwiglu>(g, rs, e, s_off[e] + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM), nb,
-                                smem);
+    const int mrows = min(kTileBM, cnt - mt * kTileBM);
+    if (mrows > kTileBM / 2)
+      wide_tile<kGather, kSwiglu, kTileBM / 32>(g, rs, e, s_off[e] + mt * kTileBM, mrows, nb, smem);
+    else
+      wide_tile<kGather, kSwiglu, kTileBM / 64>(g, rs, e, s_off[e] + mt * kTileBM, mrows, nb, smem);
     __syncthreads();
   }
 }
