@@ -62,8 +62,10 @@ def algorithmic_bytes(rows: int, touched: int) -> dict:
     return dict(layer=layer, gemm1=gemm1, gemm2=gemm2)
 
 
-PROFILE_KERNELS = {"gemm1": "grouped_gemm_kernel<true, true>",
-                   "gemm2": "grouped_gemm_kernel<false, false>"}
+# kernel names as rocprofv3 reports them: the 8-wave persistent kernel (decode-sized configs)
+# or the 4-wave WIDE kernel (many rows per expert)
+PROFILE_KERNELS = {"gemm1": ("grouped_gemm_kernel<true, true, false>", "wide_gemm_kernel<true, true>"),
+                   "gemm2": ("grouped_gemm_kernel<false, false, false>", "wide_gemm_kernel<false, false>")}
 
 
 def profiled_traffic(config_id: str, kernel: str):
@@ -72,11 +74,11 @@ def profiled_traffic(config_id: str, kernel: str):
     profiles/megamoe_layer_<config>_*.md, or None when that config has no profile."""
     import glob
 
-    name = PROFILE_KERNELS[kernel]
+    names = PROFILE_KERNELS[kernel]
     for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"megamoe_layer_{config_id}_*.md"))):
         for line in open(path):
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
-            if len(cells) == 4 and cells[0] == name and cells[3].isdigit():
+            if len(cells) == 4 and cells[0] in names and cells[3].isdigit():
                 return int(cells[3]), os.path.relpath(path, ROOT)
     return None
 
