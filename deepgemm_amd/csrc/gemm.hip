@@ -486,71 +486,74 @@ constexpr int kWideThreads = 256, kWideWaves = 4;
 constexpr int kWideBK = 128;
 constexpr int kWideStage = kTileBM * kWideBK;  // 32 KB of A
 constexpr int kWideBufs = 3;
-constexpr int kWideOut = kTileBM * 128;  // a wave's staged output tile (256 rows x 128 bytes)
-constexpr int kWideTables = kWideWaves * kWideOut > kWideBufs * kWideStage ? kWideWaves * kWideOut
-                                                                               : kWideBufs * kWideStage;
-// after the A ring / output staging: the tile's 256 row scales, then its 256 weight-row scales
-constexpr int kWideSmemBytes = kWideTables + 2 * kTileBM * 4;
+constexpr int kWideTables = kWideBufs * kWideStage;
+constexpr int kWideTableBytes = 2 * kTileBM * 4;  // a tile's 256 row scales, then its 256 weight-row scales
+// after the A ring: two scale tables (consecutive tiles of a pipelined run alternate)
+constexpr int kWideSmemBytes = kWideTables + 2 * kWideTableBytes;
 constexpr int kWideRing = 4;  // 64-k steps of B in registers
 constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that select it
 
 // Epilogue of a WIDE tile. The MFMAs run transposed (weights as the first operand), so lane
 // l holds token row tm*32 + l%32 and, per 32-column tile tn, the columns 8*(v/4) + 4*(l/32) +
 // v%4: four runs of 4 consecutive columns. The row scale is then one value per lane and row
-// tile, the column scales four 16-byte loads per column tile, and every 4 results become one
-// 8-byte bf16 write into the wave's own 32 KB of LDS (256 rows x 128 bytes, 16-byte piece p of
-// row r at piece p ^ ((r / 2) % 8): conflict-free both ways). The rows then leave as whole
-// 16-byte pieces, 8 rows per store instruction.
+// tile, the column scales four 16-byte LDS reads per column tile (both from the tile's scale
+// table), and every 4 results become one 8-byte bf16 write into the wave's 8 KB slice of a
+// free 32 KB A buffer (64 rows x 128 bytes, 16-byte piece p of row r at p ^ ((r / 2) % 8):
+// conflict-free both ways); each pass of 64 rows then leaves as whole 16-byte pieces, 8 rows
+// per store instruction.
 // GEMM1 (kGemm1) writes the pre-activation h = bf16(acc * x_scale * w_scale) [rows, 2I] with
 // gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
 // bf16 partials.
 template <bool kGather, bool kGemm1, int TM>
 __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[TM][2], int row0,
-                                           int mrows, int unit, uint8_t* wlds,
-                                           const uint8_t* tables) {
-  const int lane = opaque_tid() & (kWave - 1);
+                                           int mrows, int unit, uint8_t* stage,
+                                           const uint8_t* table) {
+  const int tid = opaque_tid();
+  const int lane = tid & (kWave - 1);
   const int rl = lane & 31, hk = lane >> 5;
-  // column scales (tile tn, run q: 4 consecutive weight rows) and row scales from the tables
-  // the prologue filled
-  const float* s_xs = reinterpret_cast<const float*>(tables);
-  const float* s_bs = s_xs + kTileBM + (opaque_tid() / kWave) * kStreamUnit;
+  const float* s_xs = reinterpret_cast<const float*>(table);
+  const float* s_bs = s_xs + kTileBM + (tid / kWave) * kStreamUnit;
   float4 bs[2][4];
 #pragma unroll
   for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
     for (int q = 0; q < 4; ++q) bs[tn][q] = *reinterpret_cast<const float4*>(s_bs + tn * 32 + q * 8 + hk * 4);
-  float xs_row[TM];
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm) xs_row[tm] = s_xs[tm * 32 + rl];
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-    const int r = tm * 32 + rl;
-    const float xs = xs_row[tm];
-    const int rkey = (r >> 1) & 7;
-#pragma unroll
-    for (int tn = 0; tn < 2; ++tn)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 ws = bs[tn][q];
-        const uint32_t lo = pack_bf16x2(acc[tm][tn][4 * q] * xs * ws.x, acc[tm][tn][4 * q + 1] * xs * ws.y);
-        const uint32_t hi = pack_bf16x2(acc[tm][tn][4 * q + 2] * xs * ws.z, acc[tm][tn][4 * q + 3] * xs * ws.w);
-        // columns tn*32 + 8q + 4hk .. +4 -> bytes 64tn + 16q + 8hk: piece 4tn + q, half hk
-        const int piece = (4 * tn + q) ^ rkey;
-        *reinterpret_cast<uint2*>(wlds + r * 128 + piece * 16 + hk * 8) = make_uint2(lo, hi);
-      }
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's LDS writes before its reads
+  uint8_t* wlds = stage + (tid / kWave) * 8192;
   const int piece = lane & 7;
   // GEMM1: pieces 0-3 are gate channels unit*32 + 8p, pieces 4-7 the up channels
   const int64_t ld = kGemm1 ? 2 * static_cast<int64_t>(g.sw.inter) : g.n;
   const int col = kGemm1 ? (piece < 4 ? unit * 32 + piece * 8 : g.sw.inter + unit * 32 + (piece - 4) * 8)
                          : unit * 64 + piece * 8;
   uint16_t* out = (kGemm1 ? reinterpret_cast<uint16_t*>(g.sw.y) : g.c) + static_cast<int64_t>(row0) * ld + col;
-#pragma unroll 8
-  for (int i = 0; i < TM * 4; ++i) {
-    const int rr = i * 8 + (lane >> 3);
-    const int4 val = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
-    if (rr < mrows) *reinterpret_cast<int4*>(out + rr * ld) = val;
+#pragma unroll
+  for (int pass = 0; pass < TM / 2; ++pass) {
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const int tm = pass * 2 + t2;
+      const float xs = s_xs[tm * 32 + rl];
+      const int r = t2 * 32 + rl;  // row within the pass
+      const int rkey = (r >> 1) & 7;
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 ws = bs[tn][q];
+          const uint32_t lo = pack_bf16x2(acc[tm][tn][4 * q] * xs * ws.x, acc[tm][tn][4 * q + 1] * xs * ws.y);
+          const uint32_t hi = pack_bf16x2(acc[tm][tn][4 * q + 2] * xs * ws.z, acc[tm][tn][4 * q + 3] * xs * ws.w);
+          // columns tn*32 + 8q + 4hk .. +4 -> bytes 64tn + 16q + 8hk: piece 4tn + q, half hk
+          const int pc = (4 * tn + q) ^ rkey;
+          *reinterpret_cast<uint2*>(wlds + r * 128 + pc * 16 + hk * 8) = make_uint2(lo, hi);
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's LDS writes before its reads
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rr = i * 8 + (lane >> 3);
+      const int4 val = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
+      const int grow = pass * 64 + rr;
+      if (grow < mrows) *reinterpret_cast<int4*>(out + grow * ld) = val;
+    }
+    // the next pass's LDS writes follow these reads in the wave's own (in-order) LDS queue
   }
 }
 
@@ -695,7 +698,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   }
   // every wave has passed its last LDS read of A (the barrier that ended the last stage)
   if (!active) return;
-  store_wide<kGather, kSwiglu, TM>(g, acc, row0, mrows, unit, smem + wave * kWideOut, smem + kWideTables);
+  store_wide<kGather, kSwiglu, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
 }
 
 // ------------------------------------------------------------------ in-kernel routing
