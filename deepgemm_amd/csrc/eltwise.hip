@@ -259,7 +259,9 @@ hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw
   if (inter % 4) return hipErrorInvalidValue;
   if (from_h && sw.row_weight == nullptr) return hipErrorInvalidValue;
   const RequantArgs r{src, sw, amax, meta, act, act_scale, inter};
-  const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 4);
+  // grid of up to 16 workgroups a CU (one row per wave in flight; the hardware keeps what fits
+  // resident): 397 us at 195,558 rows vs 470 us with 4 a CU
+  const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 16);
   if (from_h)
     hipLaunchKernelGGL(requant_kernel<true>, dim3(grid), dim3(kEltThreads), 0, stream, r);
   else
