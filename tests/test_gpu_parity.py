@@ -180,6 +180,8 @@ def test_layer_small_shapes(mm, cuda, cfg):
     torch.cuda.synchronize()
     l1c, l2c = cpu_weights(l1, l2)
     tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, activation_clamp=clamp)
+    # the shapes with many rows per expert run GEMM1 on the 4-wave kernel (bf16 h -> requant)
+    assert (buf.scratch_view("meta")[1].item() == 1) == (s * k > 8192 and s * k >= 256 * e and hdim % 256 == 0)
     _stage_checks(buf, tr, s, clamp)
     d = O.calc_diff(y.cpu(), tr.y)
     log(f"  calc_diff={d:.3e}")
@@ -219,6 +221,7 @@ def test_layer_full_shape(mm, cuda, full_weights, case):
     tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, activation_clamp=clamp,
                             unpacked_weights=unpacked)
     assert np.array_equal(stats.cpu().numpy(), tr.routing.counts)
+    assert (buf.scratch_view("meta")[1].item() == 1) == (case == "wide_2048")
     _stage_checks(buf, tr, s, clamp)
     d = O.calc_diff(y.cpu(), tr.y)
     log(f"  calc_diff={d:.3e}")
