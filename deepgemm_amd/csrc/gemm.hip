@@ -3,40 +3,45 @@
 //
 // GEMM1 (gate+up, K = H) gathers its A rows straight from the token matrix through row_token
 // (the dispatch "pull" of the reference's K1, megamoe/dcu_megamoe_large_opt/K1_fused/
-// k1_fused_ext.cu:479-746), so no grouped copy of x exists, and fuses the K2 stage
-// (megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:254-377) into its epilogue:
+// k1_fused_ext.cu:479-746), so no grouped copy of x exists:
 //   h = bf16(acc * x_sf[token] * w1_sf[e, n])       for the gate and the up column of a channel
+// On the 8-wave kernel it fuses the K2 stage (megamoe/dcu_megamoe_large_opt/K2_fused/
+// k2_fused_ext.cu:254-377) into its epilogue:
 //   y = silu(min(h_g, c)) * clamp(h_u, -c, c) * w    (fp32, left to right)
-// Each output tile holds matching gate and up channels, so SwiGLU is elementwise in registers.
-// The per-row requant (amax = max |y|; a = max(amax, 1e-4); act = e4m3(clip(y * 448/a));
-// act_scale = a/448) needs the whole row and runs as its own small kernel: a cross-workgroup
-// hand-off inside GEMM1 would need an agent-scope release per tile, which on gfx950 writes back
-// the whole (per-XCD, non-coherent) L2 -- measured 4x slower than the kernel boundary.
+// (each output tile holds matching gate and up channels, so SwiGLU is elementwise in
+// registers); on the WIDE kernel it writes h itself (bf16, the staged K1 output) and the
+// requant kernel computes y. The per-row requant (amax = max |y|; a = max(amax, 1e-4);
+// act = e4m3(clip(y * 448/a)); act_scale = a/448) needs the whole row and runs as its own small
+// kernel: a cross-workgroup hand-off inside GEMM1 would need an agent-scope release per tile,
+// which on gfx950 writes back the whole (per-XCD, non-coherent) L2 -- measured 4x slower than
+// the kernel boundary.
 // GEMM2 (down, K = I) reads act/act_scale and writes the bf16 partial rows for the combine:
 //   part[r, n] = bf16((sum_k act[r,k] * w2[e,n,k]) * act_scale[r] * w2_sf[e,n]).
 //
 // B is the Marlin nt_kpack2 weight (deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:50-66):
 // per 16-row tile, each 16-byte k-block of the 16 rows is 256 contiguous bytes.
 //
-// One persistent kernel per GEMM, one 8-wave workgroup per CU, runs two tile engines; each
-// expert's engine is chosen on the device from its routed row count:
-//  * STREAM engine (<= 64 rows: decode, HBM-bound on the weights). A workgroup tile is (expert,
-//    512 output columns, <= 64 rows) over the full K; wave w owns columns [64w, 64w + 64) and
-//    streams its weight columns from global memory into a register ring 4 steps deep (Marlin
-//    gives each lane 16 contiguous k-bytes of one weight row; 16 lanes read 256 contiguous
-//    bytes), with no barrier: B never touches LDS. The A rows, the same for the 8 waves, go to
-//    LDS once per workgroup in k-chunks of 64 KB loaded as whole 128-byte lines, double
-//    buffered: chunk c+1 is in flight while chunk c is used, and one barrier per chunk (1-4 per
-//    tile) hands the buffers over. Loading A per wave in MFMA operand order (32 lines per
-//    instruction, re-read by every wave) made the A reads, not the weights, set the pace.
-//  * TILE engine (more rows: prefill, MFMA-bound). A 256 x 256 output tile per workgroup, the
-//    8 waves as 2 x 4 with 128 x 64 each, K in 128-byte stages through double-buffered LDS
-//    (A rows XOR-swizzled, B in Marlin's own 256-byte blocks). The 256-wide tile halves the
-//    L2 bytes per FLOP of a 128-wide one, which at 4 waves per tile needed about the whole
-//    per-CU L2 bandwidth.
-// In both engines lane l supplies k-bytes [32*(l/32), 32*(l/32)+32) of each 64-k MFMA step for
-// A and B alike; any such bijection gives the same dot product, and both engines accumulate the
-// 64-k steps in the same order, so they produce the same bits.
+// Two persistent kernels per GEMM; the host picks one (gemm_wide_selected):
+//  * the 8-wave kernel (one workgroup per CU) runs two tile engines, each expert's chosen on
+//    the device from its routed row count, and can route the tasks itself (decode sizes):
+//    - STREAM engine (<= 64 rows: decode, HBM-bound on the weights). A workgroup tile is
+//      (expert, 512 output columns, <= 64 rows) over the full K; wave w owns columns
+//      [64w, 64w + 64) and streams its weight columns from global memory into a register ring
+//      4 steps deep (Marlin gives each lane 16 contiguous k-bytes of one weight row; 16 lanes
+//      read 256 contiguous bytes), with no barrier: B never touches LDS. The A rows, the same
+//      for the 8 waves, go to LDS once per workgroup in k-chunks of 64 KB loaded as whole
+//      128-byte lines, double buffered, one barrier per chunk (1-4 per tile). Loading A per
+//      wave in MFMA operand order (32 lines per instruction, re-read by every wave) made the A
+//      reads, not the weights, set the pace.
+//    - TILE engine (more rows). A 256 x 256 output tile per workgroup, the 8 waves as 2 x 4
+//      with 128 x 64 each, K in 128-byte stages through double-buffered LDS (A rows
+//      XOR-swizzled, B in Marlin's own 256-byte blocks).
+//    Both engines let lane l supply k-bytes [32*(l/32), 32*(l/32)+32) of each 64-k MFMA step
+//    for A and B alike and accumulate the 64-k steps in the same order.
+//  * the 4-wave WIDE kernel (every expert with many rows: prefill, MFMA-bound): one wave per
+//    SIMD with its 256 accumulators in AGPRs, 256 x 256 tiles, weights straight into
+//    registers and only A through LDS; described at wide_tile.
+#include <algorithm>
 #include <algorithm>
 
 #include "common.cuh"
@@ -481,15 +486,18 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
 // ring, and never touches LDS. A goes through LDS in BK = 128 stages: 256 rows of 128 bytes,
 // 16-byte piece p of row r at piece p ^ ((r / 2) % 8) (16 consecutive rows at one k hit 16
 // distinct 16-byte bank groups), three stages deep, so the first A operand of a stage is read
-// before the barrier that ends the previous one and the MFMA pipe does not drain there.
+// before the barrier that ends the previous one and the MFMA pipe does not drain there. A
+// stage's A is loaded one stage before its LDS write, spread one load or one LDS write per MFMA
+// group. Tiles are independent (prologue, stages, epilogue): a software pipeline across the
+// tiles of a workgroup needed the next tile's offsets live through the stage loop and the
+// compiler spilled (measured slower).
 constexpr int kWideThreads = 256, kWideWaves = 4;
 constexpr int kWideBK = 128;
 constexpr int kWideStage = kTileBM * kWideBK;  // 32 KB of A
 constexpr int kWideBufs = 3;
+// after the A ring: the tile's scale table (its 256 row scales, then its 256 weight-row scales)
 constexpr int kWideTables = kWideBufs * kWideStage;
-constexpr int kWideTableBytes = 2 * kTileBM * 4;  // a tile's 256 row scales, then its 256 weight-row scales
-// after the A ring: two scale tables (consecutive tiles of a pipelined run alternate)
-constexpr int kWideSmemBytes = kWideTables + 2 * kWideTableBytes;
+constexpr int kWideSmemBytes = kWideTables + 2 * kTileBM * 4;
 constexpr int kWideRing = 4;  // 64-k steps of B in registers
 constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that select it
 
