@@ -282,10 +282,14 @@ def test_layer_no_routed_rows(mm, cuda):
 
 # ------------------------------------------------------------------ graph-bucket mode
 @pytest.mark.parametrize("flag", ["big_fused_cuda_graph", "stages_fused_cuda_graph"])
-def test_graph_capture_replay_runtime_tokens(mm, cuda, flag):
+@pytest.mark.parametrize("bucket", [(200, 8), (2048, 4)])
+def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
     """Capture once at the bucket size, replay with several device token counts: every replay
-    equals an eager call on that prefix (bitwise) and leaves rows past the prefix untouched."""
-    s_max, e, hdim, inter, k = 200, 8, 512, 256, 6
+    equals an eager call on that prefix (bitwise) and leaves rows past the prefix untouched.
+    The 2048-token bucket is captured with the 4-wave WIDE GEMMs; the eager calls on the short
+    prefixes run the 8-wave kernels (same sums in the same order, so the same bits)."""
+    s_max, e = bucket
+    hdim, inter, k = 512, 256, 6
     x_fp8, x_sf, idx, w = make_tokens(s_max, hdim, e, k, seed=21, global_experts=16)
     l1, l2 = make_weights_gpu(e, hdim, inter, seed=22, mm=mm)
     buf = mm.get_symm_buffer_for_mega_moe(None, e, s_max, k, hdim, inter)
@@ -299,7 +303,7 @@ def test_graph_capture_replay_runtime_tokens(mm, cuda, flag):
     with torch.cuda.graph(graph):
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf, **{flag: True})
     ref_buf = mm.SymmBuffer(None, e, s_max, k, hdim, inter)
-    for n in (s_max, 57, 1, 0, 133):
+    for n in (s_max, 57, 1, 0, 133, s_max - 77):
         log(f"  replay with runtime tokens={n}")
         y.fill_(7.0)
         buf.cuda_graph_num_tokens.fill_(n)
