@@ -57,6 +57,7 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->y_offset = take(rows * static_cast<int64_t>(intermediate) * 4);
   l->act_offset = take(rows * static_cast<int64_t>(intermediate));
   l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
+  l->row_dest_offset = take(rows * 4);
   l->total_bytes = off;
 }
 
@@ -311,29 +312,47 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
+  mmoe::GemmArgs g2 = g1;
+  memset(&g2.sw, 0, sizeof(g2.sw));
+  g2.route_in_kernel = 0;
+  g2.a = at<uint8_t>(ws, l.act_offset);
+  g2.row_token = nullptr;
+  g2.a_scale = at<float>(ws, l.act_scale_offset);
+  g2.lda = a->intermediate;
+  g2.b = static_cast<const uint8_t*>(a->w2);
+  g2.b_scale = a->w2_sf;
+  g2.c = at<uint16_t>(ws, l.part_offset);
+  g2.n = a->hidden;
+  g2.k = a->intermediate;
+  // Prefill: rows whose token has a single routed slot leave the WIDE GEMM2 straight into y
+  // (the combine's one-term sum), so the combine neither reads nor writes them. The requant
+  // builds the row table and sets meta[2]; GEMM2 and the combine follow meta[2] on the device,
+  // so the stages behave the same in one call or in several.
+  const bool direct = mmoe::gemm_wide_selected(g2, max_rows) && l.row_capacity >= max_rows;
+  int32_t* direct_flag = at<int32_t>(ws, l.meta_offset) + 2;
+  mmoe::RowDest dest;
+  memset(&dest, 0, sizeof(dest));
+  dest.meta_flag = direct_flag;
+  if (direct) {
+    dest.row_dest = at<int32_t>(ws, l.row_dest_offset);
+    dest.row_token = at<int32_t>(ws, l.row_token_offset);
+    dest.output_index = at<int32_t>(ws, l.output_index_offset);
+    dest.topk = a->num_topk;
+    g2.row_dest = dest.row_dest;
+    g2.y_direct = static_cast<uint16_t*>(a->y);
+    g2.direct_flag = direct_flag;
+  }
+
   // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU
   if (runs(MMOE_STAGE_REQUANT) &&
       mmoe::launch_requant(at<float>(ws, l.y_offset), mmoe::gemm_wide_selected(g1, max_rows), g1.sw,
                            at<float>(ws, l.amax_offset), at<int32_t>(ws, l.meta_offset),
                            at<uint8_t>(ws, l.act_offset), at<float>(ws, l.act_scale_offset),
-                           max_rows, a->intermediate, cus, s) != hipSuccess)
+                           max_rows, a->intermediate, dest, cus, s) != hipSuccess)
     return MMOE_ERR_HIP;
 
-  if (runs(MMOE_STAGE_GEMM2)) {
-    mmoe::GemmArgs g2 = g1;
-    memset(&g2.sw, 0, sizeof(g2.sw));
-    g2.route_in_kernel = 0;
-    g2.a = at<uint8_t>(ws, l.act_offset);
-    g2.row_token = nullptr;
-    g2.a_scale = at<float>(ws, l.act_scale_offset);
-    g2.lda = a->intermediate;
-    g2.b = static_cast<const uint8_t*>(a->w2);
-    g2.b_scale = a->w2_sf;
-    g2.c = at<uint16_t>(ws, l.part_offset);
-    g2.n = a->hidden;
-    g2.k = a->intermediate;
-    if (mmoe::launch_grouped_gemm(g2, max_rows, cus, s) != hipSuccess) return MMOE_ERR_HIP;
-  }
+  if (runs(MMOE_STAGE_GEMM2) && mmoe::launch_grouped_gemm(g2, max_rows, cus, s) != hipSuccess)
+    return MMOE_ERR_HIP;
 
   if (runs(MMOE_STAGE_COMBINE)) {
     mmoe::CombineArgs c;
@@ -345,6 +364,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     c.host_tokens = a->num_tokens;
     c.topk = a->num_topk;
     c.hidden = a->hidden;
+    c.skip_single = direct_flag;
     if (mmoe::launch_combine(c, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   }
   return MMOE_OK;

@@ -35,6 +35,7 @@ struct RequantArgs {
   uint8_t* act;
   float* act_scale;
   int inter;
+  RowDest dest;
 };
 
 // channels 4q .. 4q+3 of row `row`
@@ -58,9 +59,13 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
   const int wave = threadIdx.x / kWave;
   const int rows = r.meta[0];
   const int groups = r.inter >> 2;
-  if (blockIdx.x == 0 && threadIdx.x == 0) r.meta[1] = kFromH ? 1 : 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    r.meta[1] = kFromH ? 1 : 0;
+    if (r.dest.meta_flag != nullptr) *r.dest.meta_flag = r.dest.row_dest != nullptr ? 1 : 0;
+  }
   for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
     const float w = kFromH ? r.sw.row_weight[row] : 0.0f;
+    const int tok = r.dest.row_dest != nullptr ? r.dest.row_token[row] : 0;
     uint32_t* ar = reinterpret_cast<uint32_t*>(r.act + static_cast<int64_t>(row) * r.inter);
     float m = 0.0f;
     if (groups <= kRequantGroups * kWave) {
@@ -87,6 +92,13 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
         ar[q] = pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
       }
     }
+    if (r.dest.row_dest != nullptr) {
+      // the row's token has exactly one routed slot: GEMM2 writes its output row straight to y
+      const int slot_row = lane < r.dest.topk
+          ? r.dest.output_index[static_cast<int64_t>(tok) * r.dest.topk + lane] : -1;
+      const int routed = __popcll(__ballot(slot_row >= 0));
+      if (lane == 0) r.dest.row_dest[row] = routed == 1 ? tok : -1;
+    }
     if (lane == 0) {
       r.amax[row] = m;
       r.act_scale[row] = fmaxf(m, kAmaxFloor) / kE4m3Max;
@@ -95,53 +107,86 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
 }
 
 // ---------------------------------------------------------------- combine
-// One workgroup per token (grid-stride); each thread owns 8-element (16-byte) columns.
+// One wave per (token, piece of V*64 16-byte column groups), grid-stride over those items; the
+// next item's slot rows are loaded while the current one is summed, so an item costs one round
+// trip per routed slot. Lanes 0..K-1 hold the token's slot rows; every lane owns the 16-byte
+// groups lane + 64j of the piece. Slots are summed in ascending order into fp32 accumulators
+// that start at +0 (the reference's order); a token without routed slots gets zeros, and with
+// skip_single a token with exactly one routed slot is left alone (GEMM2 wrote that row to y).
+// V = 8 (whole 4096-column rows) for many tokens; V = 2 spreads few tokens over more waves.
+template <int V>
 __global__ __launch_bounds__(kEltThreads) void combine_kernel(CombineArgs c) {
-  __shared__ int s_rows[16];
-  __shared__ float s_w[16];
+  const int lane = lane_id();
   const int tokens = effective_tokens(c.runtime_tokens, c.host_tokens);
   const int nvec = c.hidden >> 3;
-  for (int t = blockIdx.x; t < tokens; t += gridDim.x) {
-    if (threadIdx.x < c.topk) {
-      const int64_t route = static_cast<int64_t>(t) * c.topk + threadIdx.x;
-      int row = c.output_index[route];
-      float w = 1.0f;
-      if (c.topk_ids != nullptr) {
-        const int64_t ex = c.ids_i64 ? static_cast<const int64_t*>(c.topk_ids)[route]
-                                     : static_cast<const int32_t*>(c.topk_ids)[route];
-        if (ex < 0) row = -1;
-      }
-      if (c.apply_weights) w = c.topk_w[route];
-      s_rows[threadIdx.x] = row;
-      s_w[threadIdx.x] = w;
+  const int parts = (nvec + kWave * V - 1) / (kWave * V);
+  const int64_t items = static_cast<int64_t>(tokens) * parts;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kEltWaves;
+  int64_t it = static_cast<int64_t>(blockIdx.x) * kEltWaves + threadIdx.x / kWave;
+  // lane < K: the row of slot `lane` of item i's token (-1: not routed) and its weight
+  auto slot_row = [&](int64_t i, float& w) {
+    w = 1.0f;
+    if (i >= items || lane >= c.topk) return -1;
+    const int64_t route = (i / parts) * c.topk + lane;
+    int row = c.output_index[route];
+    if (c.topk_ids != nullptr) {
+      const int64_t ex = c.ids_i64 ? static_cast<const int64_t*>(c.topk_ids)[route]
+                                   : static_cast<const int32_t*>(c.topk_ids)[route];
+      if (ex < 0) row = -1;
     }
-    __syncthreads();
-    uint4* yrow = reinterpret_cast<uint4*>(c.y + static_cast<int64_t>(t) * c.hidden);
-    for (int v = threadIdx.x; v < nvec; v += kEltThreads) {
-      float sum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < c.topk; ++s) {
-        const int row = s_rows[s];
-        if (row < 0) continue;
-        const uint4 p = reinterpret_cast<const uint4*>(c.part + static_cast<int64_t>(row) * c.hidden)[v];
-        const uint32_t words[4] = {p.x, p.y, p.z, p.w};
-        const float w = s_w[s];
+    if (c.apply_weights) w = c.topk_w[route];
+    return row;
+  };
+  const bool skip_single = c.skip_single != nullptr && *c.skip_single != 0;
+  float w;
+  int row = slot_row(it, w);
+  for (; it < items; it += stride) {
+    float next_w;
+    const int next_row = slot_row(it + stride, next_w);
+    const uint64_t routed = __ballot(row >= 0);
+    if (!(skip_single && __popcll(routed) == 1)) {
+      const int64_t t = it / parts;
+      const int v0 = static_cast<int>(it - t * parts) * kWave * V;
+      float sum[V][8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float lo = bf16_to_f32(words[q] & 0xffff);
-          float hi = bf16_to_f32(words[q] >> 16);
-          if (c.apply_weights) { lo *= w; hi *= w; }
-          sum[2 * q] += lo;
-          sum[2 * q + 1] += hi;
+      for (int j = 0; j < V; ++j)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) sum[j][q] = 0.0f;
+      for (uint64_t m = routed; m != 0; m &= m - 1) {
+        const int s = __ffsll(static_cast<unsigned long long>(m)) - 1;
+        const int r = __shfl(row, s, kWave);
+        const float ws = __shfl(w, s, kWave);
+        const uint4* prow = reinterpret_cast<const uint4*>(c.part + static_cast<int64_t>(r) * c.hidden);
+        uint4 p[V];
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const int v = v0 + j * kWave + lane;
+          p[j] = v < nvec ? prow[v] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          const uint32_t words[4] = {p[j].x, p[j].y, p[j].z, p[j].w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float lo = bf16_to_f32(words[q] & 0xffff);
+            float hi = bf16_to_f32(words[q] >> 16);
+            if (c.apply_weights) { lo *= ws; hi *= ws; }
+            sum[j][2 * q] += lo;
+            sum[j][2 * q + 1] += hi;
+          }
         }
       }
-      uint4 o;
-      o.x = pack_bf16x2(sum[0], sum[1]);
-      o.y = pack_bf16x2(sum[2], sum[3]);
-      o.z = pack_bf16x2(sum[4], sum[5]);
-      o.w = pack_bf16x2(sum[6], sum[7]);
-      yrow[v] = o;
+      uint4* yrow = reinterpret_cast<uint4*>(c.y + t * c.hidden);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int v = v0 + j * kWave + lane;
+        if (v < nvec)
+          yrow[v] = make_uint4(pack_bf16x2(sum[j][0], sum[j][1]), pack_bf16x2(sum[j][2], sum[j][3]),
+                               pack_bf16x2(sum[j][4], sum[j][5]), pack_bf16x2(sum[j][6], sum[j][7]));
+      }
     }
-    __syncthreads();
+    row = next_row;
+    w = next_w;
   }
 }
 
@@ -254,11 +299,14 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 
 hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw, float* amax,
                           int32_t* meta, uint8_t* act, float* act_scale, int64_t max_rows,
-                          int inter, int num_cus, hipStream_t stream) {
+                          int inter, const RowDest& dest, int num_cus, hipStream_t stream) {
   if (max_rows <= 0) return hipSuccess;
   if (inter % 4) return hipErrorInvalidValue;
   if (from_h && sw.row_weight == nullptr) return hipErrorInvalidValue;
-  const RequantArgs r{src, sw, amax, meta, act, act_scale, inter};
+  if (dest.row_dest != nullptr && (dest.row_token == nullptr || dest.output_index == nullptr ||
+                                   dest.topk < 1 || dest.topk > kWave))
+    return hipErrorInvalidValue;
+  const RequantArgs r{src, sw, amax, meta, act, act_scale, inter, dest};
   // grid of up to 16 workgroups a CU (one row per wave in flight; the hardware keeps what fits
   // resident): 397 us at 195,558 rows vs 470 us with 4 a CU
   const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 16);
@@ -272,10 +320,22 @@ hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream) {
   if (c.host_tokens <= 0) return hipSuccess;
   if (c.topk > 16) return hipErrorInvalidValue;
-  const unsigned grid = grid_for(c.host_tokens, 1, static_cast<int64_t>(num_cus) * 16);
   if ((c.hidden & 7) == 0) {
-    hipLaunchKernelGGL(combine_kernel, dim3(grid), dim3(kEltThreads), 0, stream, c);
+    // a wave per item, up to 8 four-wave workgroups a CU in flight; whole rows once there are
+    // at least 16 tokens a CU
+    const int64_t nvec = c.hidden >> 3;
+    if (c.host_tokens >= static_cast<int64_t>(num_cus) * 16) {
+      const int64_t items = c.host_tokens * ((nvec + kWave * 8 - 1) / (kWave * 8));
+      const unsigned grid = grid_for(items, kEltWaves, static_cast<int64_t>(num_cus) * 8);
+      hipLaunchKernelGGL(combine_kernel<8>, dim3(grid), dim3(kEltThreads), 0, stream, c);
+    } else {
+      const int64_t items = c.host_tokens * ((nvec + kWave * 2 - 1) / (kWave * 2));
+      const unsigned grid = grid_for(items, kEltWaves, static_cast<int64_t>(num_cus) * 8);
+      hipLaunchKernelGGL(combine_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, c);
+    }
   } else {
+    if (c.skip_single != nullptr) return hipErrorInvalidValue;
+    const unsigned grid = grid_for(c.host_tokens, 1, static_cast<int64_t>(num_cus) * 16);
     hipLaunchKernelGGL(combine_scalar_kernel, dim3(grid), dim3(kEltThreads), 0, stream, c);
   }
   return hipGetLastError();

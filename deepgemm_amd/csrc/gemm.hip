@@ -497,9 +497,19 @@ constexpr int kWideStage = kTileBM * kWideBK;  // 32 KB of A
 constexpr int kWideBufs = 3;
 // after the A ring: the tile's scale table (its 256 row scales, then its 256 weight-row scales)
 constexpr int kWideTables = kWideBufs * kWideStage;
-constexpr int kWideSmemBytes = kWideTables + 2 * kTileBM * 4;
+constexpr int kWideSmemBytes = kWideTables + 3 * kTileBM * 4;
 constexpr int kWideRing = 4;  // 64-k steps of B in registers
 constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that select it
+
+// bf16 -0 -> +0 in both halves: the combine's sum starts at +0, so a one-term sum of -0 is +0.
+// m = u ^ 0x80008000 has a half of 0 exactly where u has -0; (m & 0x7fff7fff) + 0x7fff7fff sets
+// bit 15 (31) of a half unless its magnitude is 0 (no carry crosses the halves).
+__device__ __forceinline__ int plus_zero_bf16x2(int v) {
+  const uint32_t u = static_cast<uint32_t>(v);
+  const uint32_t m = u ^ 0x80008000u;
+  const uint32_t nonzero = ((m & 0x7fff7fffu) + 0x7fff7fffu) | m;
+  return static_cast<int>(u & (nonzero | 0x7fff7fffu));
+}
 
 // Epilogue of a WIDE tile. The MFMAs run transposed (weights as the first operand), so lane
 // l holds token row tm*32 + l%32 and, per 32-column tile tn, the columns 8*(v/4) + 4*(l/32) +
@@ -511,7 +521,8 @@ constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that sele
 // per store instruction.
 // GEMM1 (kGemm1) writes the pre-activation h = bf16(acc * x_scale * w_scale) [rows, 2I] with
 // gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
-// bf16 partials.
+// bf16 partials (-0 as +0), a row whose token has no other routed slot straight into y
+// (row_dest).
 template <bool kGather, bool kGemm1, int TM>
 __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[TM][2], int row0,
                                            int mrows, int unit, uint8_t* stage,
@@ -521,6 +532,7 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
   const int rl = lane & 31, hk = lane >> 5;
   const float* s_xs = reinterpret_cast<const float*>(table);
   const float* s_bs = s_xs + kTileBM + (tid / kWave) * kStreamUnit;
+  const int* s_dest = reinterpret_cast<const int*>(table) + 2 * kTileBM;  // -1: not direct
   float4 bs[2][4];
 #pragma unroll
   for (int tn = 0; tn < 2; ++tn)
@@ -533,6 +545,8 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
   const int col = kGemm1 ? (piece < 4 ? unit * 32 + piece * 8 : g.sw.inter + unit * 32 + (piece - 4) * 8)
                          : unit * 64 + piece * 8;
   uint16_t* out = (kGemm1 ? reinterpret_cast<uint16_t*>(g.sw.y) : g.c) + static_cast<int64_t>(row0) * ld + col;
+  const uint64_t y_col = reinterpret_cast<uint64_t>(g.y_direct + col);  // GEMM2 direct rows
+  const uint64_t y_pitch = static_cast<uint64_t>(ld) * 2;
 #pragma unroll
   for (int pass = 0; pass < TM / 2; ++pass) {
 #pragma unroll
@@ -554,12 +568,32 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
         }
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's LDS writes before its reads
+    int4 val[8];
+    int dest[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int rr = i * 8 + (lane >> 3);
-      const int4 val = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
-      const int grow = pass * 64 + rr;
-      if (grow < mrows) *reinterpret_cast<int4*>(out + grow * ld) = val;
+      val[i] = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
+      if (!kGemm1) dest[i] = s_dest[pass * 64 + rr];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int grow = pass * 64 + i * 8 + (lane >> 3);
+      if (kGemm1) {
+        if (grow < mrows) *reinterpret_cast<int4*>(out + grow * ld) = val[i];
+      } else {
+        // a row whose token has no other routed slot goes to y (its output is the layer
+        // output): both addresses computed, one selected (no branch: the LDS reads above stay
+        // batched and the 16-byte store whole). -0 becomes +0 in every GEMM2 row: the
+        // combine's sums (from +0) cannot tell them apart
+        const uint64_t to_y = y_col + static_cast<uint64_t>(static_cast<uint32_t>(dest[i])) * y_pitch;
+        const uint64_t to_part = reinterpret_cast<uint64_t>(out + grow * ld);
+        const uint64_t addr = dest[i] >= 0 ? to_y : to_part;
+        const i32x4 v = {plus_zero_bf16x2(val[i].x), plus_zero_bf16x2(val[i].y),
+                         plus_zero_bf16x2(val[i].z), plus_zero_bf16x2(val[i].w)};
+        // a global (not flat) store: a flat one would also hold up the LDS counter
+        if (grow < mrows) *(__attribute__((address_space(1))) i32x4*)(addr) = v;
+      }
     }
     // the next pass's LDS writes follow these reads in the wave's own (in-order) LDS queue
   }
@@ -679,6 +713,12 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   // its wave's column lane), A stages 0 and 1 into LDS, stage 2 into register set 0, B steps
   // 0..3, the first operands. Rows past mrows take the last row's scale (never stored).
   const float pre_xs = row_scale<kGather>(g, rs, row0 + min(tid, mrows - 1));
+  // direct rows: the switch and the row table load side by side (no dependent round trip)
+  int pre_dest = -1, pre_on = 0;
+  if (!kSwiglu && g.y_direct != nullptr) {
+    pre_on = *g.direct_flag;
+    pre_dest = g.row_dest[row0 + min(tid, mrows - 1)];
+  }
   const float pre_bs = g.b_scale[static_cast<int64_t>(e) * g.n + weight_row<kSwiglu>(g, unit, kStreamUnit, lane)];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) load_a(0, i, 0);
@@ -694,6 +734,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   for (int i = 0; i < kALoads; ++i) store_a(1, i, 1);
   reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
   reinterpret_cast<float*>(smem + kWideTables)[kTileBM + tid] = pre_bs;
+  if (!kSwiglu) reinterpret_cast<int*>(smem + kWideTables)[2 * kTileBM + tid] = pre_on != 0 ? pre_dest : -1;
   lds_barrier();
 #pragma unroll
   for (int gi = 0; gi < kAhead; ++gi) abuf[gi] = read_group(0, gi);
@@ -1112,6 +1153,9 @@ hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hip
   if (g.num_experts > kMaxGemmExperts) return hipErrorInvalidValue;
   const bool wide = gemm_wide_selected(g, max_rows);
   if (wide && g.route_in_kernel) return hipErrorInvalidValue;
+  // direct writes to y: the WIDE GEMM2 epilogue only
+  if (g.y_direct != nullptr && (!wide || g.sw.enabled || g.row_dest == nullptr || g.direct_flag == nullptr))
+    return hipErrorInvalidValue;
   if (g.sw.enabled) {
     if (g.row_token == nullptr || g.n != 2 * g.sw.inter) return hipErrorInvalidValue;
     return wide ? launch_wide<true, true>(g, max_rows, num_cus, stream)

@@ -67,6 +67,12 @@ struct GemmArgs {
   SwigluEpilogue sw;         // GEMM1 only (requires row_token); c is unused then
   int route_in_kernel;       // GEMM1: route the tasks in the kernel (<= gemm_route_max_tasks())
   RouteArgs route;           // the routing to do then (counts, offsets, row tables are written)
+  // GEMM2 on the WIDE kernel, when *direct_flag != 0: rows with row_dest[r] >= 0 go to
+  // y_direct[row_dest[r]] (bf16 [S, N], a negative zero stored as +0 like the combine's sum)
+  // instead of c. Null pointers: every row to c.
+  const int32_t* row_dest;
+  uint16_t* y_direct;
+  const int32_t* direct_flag;
 };
 
 // Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
@@ -81,17 +87,32 @@ bool gemm_wide_selected(const GemmArgs& g, int max_rows);
 int gemm_route_max_tasks();
 int gemm_route_max_experts();
 
+// Rows whose token has exactly one routed slot: their GEMM2 output is the layer output (the
+// combine's one-term sum), so GEMM2 can write it straight into y. row_dest[r] = the token of
+// row r if so, else -1 (built by the requant from output_index); *meta_flag = 1 when built,
+// 0 when not (GEMM2 and the combine read it).
+struct RowDest {
+  int32_t* row_dest;             // [rows] or null (not built)
+  const int32_t* row_token;      // [rows]
+  const int32_t* output_index;   // [S, K]
+  int topk;
+  int32_t* meta_flag;
+};
+
 // Per-row requant of the SwiGLU output: amax = max |y| (written out), a = max(amax, 1e-4);
 // act = e4m3(clip(y * 448/a)); act_scale = a/448 -- for rows < meta[0]. y is GEMM1's fp32
 // SwiGLU output, or with from_h the SwiGLU of GEMM1's bf16 pre-activation h [rows, 2I]
-// computed here (sw: route weights and clamp). meta[1] records which (1 = from h).
+// computed here (sw: route weights and clamp). meta[1] records which (1 = from h). With
+// dest.row_dest it also builds the direct-write table (RowDest).
 hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw, float* amax,
                           int32_t* meta, uint8_t* act, float* act_scale, int64_t max_rows,
-                          int inter, int num_cus, hipStream_t stream);
+                          int inter, const RowDest& dest, int num_cus, hipStream_t stream);
 
 struct CombineArgs {
   uint16_t* y;                     // bf16 [S, H]
   const uint16_t* part;            // bf16 [rows, H]
+  const int32_t* skip_single;      // null, or *skip_single != 0: tokens with exactly one
+                                   // routed slot were written by GEMM2 (RowDest)
   const int32_t* output_index;     // [S, K]
   const void* topk_ids;            // optional validity/weight source (postprocess)
   int ids_i64;

@@ -275,7 +275,9 @@ class SymmBuffer:
     def scratch_view(self, name: str, num_rows: Optional[int] = None) -> torch.Tensor:
         """Intermediate tensors of the last call: counts, offsets, meta, output_index,
         row_token, row_weight, m_indices, act_scale, amax (max |y| per row), y (SwiGLU x
-        weight, f32), act (requantised y), part (GEMM2 rows). When meta[1] == 1 the GEMM1 of
+        weight, f32), act (requantised y), part (GEMM2 rows), row_dest (the token whose y
+        row GEMM2 wrote directly for a row, else -1; built in calls with the WIDE GEMMs, where
+        those rows' part is not written; meta[2] == 1 then). When meta[1] == 1 the GEMM1 of
         the call left the bf16 pre-activation instead of y, in the same bytes: view it as h
         ([rows, 2I], gate channels then up channels)."""
         l = self.scratch_layout
@@ -295,6 +297,7 @@ class SymmBuffer:
             "h": (l.y_offset, torch.bfloat16, (rows, 2 * self.intermediate_hidden)),
             "act": (l.act_offset, torch.float8_e4m3fn, (rows, self.intermediate_hidden)),
             "part": (l.part_offset, torch.bfloat16, (rows, self.hidden)),
+            "row_dest": (l.row_dest_offset, torch.int32, (rows,)),
         }
         off, dtype, shape = spec[name]
         n = 1

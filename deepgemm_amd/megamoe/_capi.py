@@ -51,6 +51,7 @@ class ScratchLayout(ctypes.Structure):
         ("y_offset", c_i64),
         ("act_offset", c_i64),
         ("part_offset", c_i64),
+        ("row_dest_offset", c_i64),
     ]
 
 

@@ -76,7 +76,9 @@ typedef struct mmoe_scratch_layout {
   int64_t num_chunks;          /* routing chunks of MMOE_ROUTE_CHUNK tasks */
   int64_t counts_offset;       /* int32 [E]   rows per local expert */
   int64_t offsets_offset;      /* int32 [E+1] first row of each expert (exclusive scan) */
-  int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R */
+  int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R; [1] = 1: GEMM1 left
+                                  the bf16 pre-activation h in y's bytes; [2] = 1: GEMM2 wrote
+                                  the rows of single-slot tokens straight to y (row_dest) */
   int64_t chunk_counts_offset; /* int32 [num_chunks, E] */
   int64_t output_index_offset; /* int32 [S_max, K]  row of (token, slot) or -1 */
   int64_t row_token_offset;    /* int32 [rows] source token of each routed row */
@@ -86,7 +88,11 @@ typedef struct mmoe_scratch_layout {
   int64_t amax_offset;         /* f32   [rows] max |y| per row (written by the requant stage) */
   int64_t y_offset;            /* f32   [rows, I]  SwiGLU x weight output of GEMM1 */
   int64_t act_offset;          /* e4m3  [rows, I]  requantised SwiGLU output */
-  int64_t part_offset;         /* bf16  [rows, H]  per-row GEMM2 output (combine partials) */
+  int64_t part_offset;         /* bf16  [rows, H]  per-row GEMM2 output (combine partials);
+                                  in a prefill call (WIDE GEMMs) the rows of tokens with a
+                                  single routed slot go straight to y instead (row_dest) */
+  int64_t row_dest_offset;     /* int32 [rows] token of a row written straight to y, else -1
+                                  (valid after a call that used it) */
 } mmoe_scratch_layout;
 
 #define MMOE_ROUTE_CHUNK 1024

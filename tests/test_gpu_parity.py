@@ -157,7 +157,36 @@ def _stage_checks(buf, tr, s, clamp=None):
     deq_ref = tr.act.float() * tr.act_scale.view(-1, 1)
     assert O.calc_diff(deq, deq_ref) < 1e-4, "SwiGLU requant"
     part = buf.scratch_view("part")[:r].cpu()
-    assert O.calc_diff(part, tr.part) < 1e-3, "GEMM2 partials"
+    if buf.scratch_view("meta")[2].item() == 1:
+        # GEMM2 wrote the rows of single-slot tokens straight to y: row_dest names exactly those
+        # rows (their token), and part holds the others
+        row_dest = buf.scratch_view("row_dest")[:r].cpu().numpy()
+        tok = np.asarray(tr.routing.row_token)[:r]
+        slots = (np.asarray(tr.routing.output_index) >= 0).sum(axis=1)
+        assert np.array_equal(row_dest, np.where(slots[tok] == 1, tok, -1)), "row_dest"
+        keep = torch.from_numpy(row_dest < 0)
+        assert O.calc_diff(part[keep], tr.part[keep]) < 1e-3, "GEMM2 partials"
+    else:
+        assert O.calc_diff(part, tr.part) < 1e-3, "GEMM2 partials"
+
+
+def _combine_bitwise(mm, buf, y, l1, l2, s, clamp):
+    """y is bitwise the slot-ordered fp32 sum (bf16 RNE) of GEMM2's own rows. When GEMM2 wrote
+    single-slot tokens straight to y (meta[2] == 1), GEMM2 runs again with that switched off
+    (meta[2] = 0, its only input besides the row table) so that every row is in part: this
+    pins the direct rows (a one-term sum, -0 stored as +0) and the combine alike."""
+    meta = buf.scratch_view("meta")
+    if meta[2].item() == 1:
+        meta[2] = 0
+        mm.LayerCall(torch.empty_like(y), l1, l2, buf, activation_clamp=clamp).run(3, 3)
+        torch.cuda.synchronize()
+    r = int(meta[0].item())
+    part = buf.scratch_view("part")[:r].cpu()
+    oi = buf.scratch_view("output_index")[:s].cpu().numpy()
+    expect = O.combine(part, oi, s)
+    got = y.cpu()
+    bad = (got.view(torch.int16) != expect.view(torch.int16)).nonzero()
+    assert bad.numel() == 0, f"combine not bitwise at {bad[:8].tolist()}"
 
 
 @pytest.mark.parametrize("cfg", [
@@ -169,6 +198,8 @@ def _stage_checks(buf, tr, s, clamp=None):
     # on the 8-wave kernel because k % 256 != 0), then both GEMMs on it with ragged row blocks
     (2048, 4, 640, 256, 6, 16, None),
     (1500, 5, 768, 256, 6, 8, None),
+    # >= 16 tokens a CU: the whole-row combine; most tokens have one routed slot (direct rows)
+    (4500, 4, 256, 256, 2, 16, None),
 ])
 def test_layer_small_shapes(mm, cuda, cfg):
     s, e, hdim, inter, k, g, clamp = cfg
@@ -182,7 +213,10 @@ def test_layer_small_shapes(mm, cuda, cfg):
     tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, activation_clamp=clamp)
     # the shapes with many rows per expert run GEMM1 on the 4-wave kernel (bf16 h -> requant)
     assert (buf.scratch_view("meta")[1].item() == 1) == (s * k > 8192 and s * k >= 256 * e and hdim % 256 == 0)
+    # GEMM2 (k = I) on the 4-wave kernel writes single-slot tokens straight to y
+    assert (buf.scratch_view("meta")[2].item() == 1) == (s * k > 8192 and s * k >= 256 * e and inter % 256 == 0)
     _stage_checks(buf, tr, s, clamp)
+    _combine_bitwise(mm, buf, y, l1, l2, s, clamp)
     d = O.calc_diff(y.cpu(), tr.y)
     log(f"  calc_diff={d:.3e}")
     assert d <= CALC_DIFF_BAR
@@ -222,7 +256,9 @@ def test_layer_full_shape(mm, cuda, full_weights, case):
                             unpacked_weights=unpacked)
     assert np.array_equal(stats.cpu().numpy(), tr.routing.counts)
     assert (buf.scratch_view("meta")[1].item() == 1) == (case == "wide_2048")
+    assert (buf.scratch_view("meta")[2].item() == 1) == (case == "wide_2048")
     _stage_checks(buf, tr, s, clamp)
+    _combine_bitwise(mm, buf, y, l1, l2, s, clamp)
     d = O.calc_diff(y.cpu(), tr.y)
     log(f"  calc_diff={d:.3e}")
     assert d <= CALC_DIFF_BAR
