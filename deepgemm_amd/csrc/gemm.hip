@@ -497,19 +497,10 @@ constexpr int kWideStage = kTileBM * kWideBK;  // 32 KB of A
 constexpr int kWideBufs = 3;
 // after the A ring: the tile's scale table (its 256 row scales, then its 256 weight-row scales)
 constexpr int kWideTables = kWideBufs * kWideStage;
-constexpr int kWideSmemBytes = kWideTables + 3 * kTileBM * 4;
+// the tables: 256 row scales, 256 weight-row scales (f32), then (GEMM2) 256 row addresses (u64)
+constexpr int kWideSmemBytes = kWideTables + 2 * kTileBM * 4 + kTileBM * 8;
 constexpr int kWideRing = 4;  // 64-k steps of B in registers
 constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that select it
-
-// bf16 -0 -> +0 in both halves: the combine's sum starts at +0, so a one-term sum of -0 is +0.
-// m = u ^ 0x80008000 has a half of 0 exactly where u has -0; (m & 0x7fff7fff) + 0x7fff7fff sets
-// bit 15 (31) of a half unless its magnitude is 0 (no carry crosses the halves).
-__device__ __forceinline__ int plus_zero_bf16x2(int v) {
-  const uint32_t u = static_cast<uint32_t>(v);
-  const uint32_t m = u ^ 0x80008000u;
-  const uint32_t nonzero = ((m & 0x7fff7fffu) + 0x7fff7fffu) | m;
-  return static_cast<int>(u & (nonzero | 0x7fff7fffu));
-}
 
 // Epilogue of a WIDE tile. The MFMAs run transposed (weights as the first operand), so lane
 // l holds token row tm*32 + l%32 and, per 32-column tile tn, the columns 8*(v/4) + 4*(l/32) +
@@ -521,8 +512,8 @@ __device__ __forceinline__ int plus_zero_bf16x2(int v) {
 // per store instruction.
 // GEMM1 (kGemm1) writes the pre-activation h = bf16(acc * x_scale * w_scale) [rows, 2I] with
 // gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
-// bf16 partials (-0 as +0), a row whose token has no other routed slot straight into y
-// (row_dest).
+// bf16 partials (-0 as +0) to the row addresses of the tile's table: its part row, or for a
+// row whose token has no other routed slot its y row (row_dest).
 template <bool kGather, bool kGemm1, int TM>
 __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[TM][2], int row0,
                                            int mrows, int unit, uint8_t* stage,
@@ -532,7 +523,7 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
   const int rl = lane & 31, hk = lane >> 5;
   const float* s_xs = reinterpret_cast<const float*>(table);
   const float* s_bs = s_xs + kTileBM + (tid / kWave) * kStreamUnit;
-  const int* s_dest = reinterpret_cast<const int*>(table) + 2 * kTileBM;  // -1: not direct
+  const uint64_t* s_addr = reinterpret_cast<const uint64_t*>(table + 2 * kTileBM * 4);  // GEMM2
   float4 bs[2][4];
 #pragma unroll
   for (int tn = 0; tn < 2; ++tn)
@@ -545,8 +536,6 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
   const int col = kGemm1 ? (piece < 4 ? unit * 32 + piece * 8 : g.sw.inter + unit * 32 + (piece - 4) * 8)
                          : unit * 64 + piece * 8;
   uint16_t* out = (kGemm1 ? reinterpret_cast<uint16_t*>(g.sw.y) : g.c) + static_cast<int64_t>(row0) * ld + col;
-  const uint64_t y_col = reinterpret_cast<uint64_t>(g.y_direct + col);  // GEMM2 direct rows
-  const uint64_t y_pitch = static_cast<uint64_t>(ld) * 2;
 #pragma unroll
   for (int pass = 0; pass < TM / 2; ++pass) {
 #pragma unroll
@@ -560,8 +549,11 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float4 ws = bs[tn][q];
-          const uint32_t lo = pack_bf16x2(acc[tm][tn][4 * q] * xs * ws.x, acc[tm][tn][4 * q + 1] * xs * ws.y);
-          const uint32_t hi = pack_bf16x2(acc[tm][tn][4 * q + 2] * xs * ws.z, acc[tm][tn][4 * q + 3] * xs * ws.w);
+          // GEMM2: the scale product as fma(., ., +0), the same rounding, but a zero is +0 (the
+          // combine's sum from +0 writes +0 too, so a y row written here matches it bitwise)
+          auto scaled = [&](float a, float w) { return kGemm1 ? a * xs * w : __builtin_fmaf(a * xs, w, 0.0f); };
+          const uint32_t lo = pack_bf16x2(scaled(acc[tm][tn][4 * q], ws.x), scaled(acc[tm][tn][4 * q + 1], ws.y));
+          const uint32_t hi = pack_bf16x2(scaled(acc[tm][tn][4 * q + 2], ws.z), scaled(acc[tm][tn][4 * q + 3], ws.w));
           // columns tn*32 + 8q + 4hk .. +4 -> bytes 64tn + 16q + 8hk: piece 4tn + q, half hk
           const int pc = (4 * tn + q) ^ rkey;
           *reinterpret_cast<uint2*>(wlds + r * 128 + pc * 16 + hk * 8) = make_uint2(lo, hi);
@@ -569,12 +561,12 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's LDS writes before its reads
     int4 val[8];
-    int dest[8];
+    uint64_t base[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int rr = i * 8 + (lane >> 3);
       val[i] = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
-      if (!kGemm1) dest[i] = s_dest[pass * 64 + rr];
+      if (!kGemm1) base[i] = s_addr[pass * 64 + rr];
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -582,17 +574,10 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
       if (kGemm1) {
         if (grow < mrows) *reinterpret_cast<int4*>(out + grow * ld) = val[i];
       } else {
-        // a row whose token has no other routed slot goes to y (its output is the layer
-        // output): both addresses computed, one selected (no branch: the LDS reads above stay
-        // batched and the 16-byte store whole). -0 becomes +0 in every GEMM2 row: the
-        // combine's sums (from +0) cannot tell them apart
-        const uint64_t to_y = y_col + static_cast<uint64_t>(static_cast<uint32_t>(dest[i])) * y_pitch;
-        const uint64_t to_part = reinterpret_cast<uint64_t>(out + grow * ld);
-        const uint64_t addr = dest[i] >= 0 ? to_y : to_part;
-        const i32x4 v = {plus_zero_bf16x2(val[i].x), plus_zero_bf16x2(val[i].y),
-                         plus_zero_bf16x2(val[i].z), plus_zero_bf16x2(val[i].w)};
-        // a global (not flat) store: a flat one would also hold up the LDS counter
-        if (grow < mrows) *(__attribute__((address_space(1))) i32x4*)(addr) = v;
+        // the row's address from the table (its part row or its token's y row); a global (not
+        // flat) store: a flat one would also hold up the LDS counter
+        const i32x4 v = {val[i].x, val[i].y, val[i].z, val[i].w};
+        if (grow < mrows) *(__attribute__((address_space(1))) i32x4*)(base[i] + col * 2) = v;
       }
     }
     // the next pass's LDS writes follow these reads in the wave's own (in-order) LDS queue
@@ -713,7 +698,8 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   // its wave's column lane), A stages 0 and 1 into LDS, stage 2 into register set 0, B steps
   // 0..3, the first operands. Rows past mrows take the last row's scale (never stored).
   const float pre_xs = row_scale<kGather>(g, rs, row0 + min(tid, mrows - 1));
-  // direct rows: the switch and the row table load side by side (no dependent round trip)
+  // GEMM2: row tid's output address (its part row, or its token's y row when the token has no
+  // other routed slot and direct rows are on); the switch and the row table load side by side
   int pre_dest = -1, pre_on = 0;
   if (!kSwiglu && g.y_direct != nullptr) {
     pre_on = *g.direct_flag;
@@ -734,7 +720,12 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   for (int i = 0; i < kALoads; ++i) store_a(1, i, 1);
   reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
   reinterpret_cast<float*>(smem + kWideTables)[kTileBM + tid] = pre_bs;
-  if (!kSwiglu) reinterpret_cast<int*>(smem + kWideTables)[2 * kTileBM + tid] = pre_on != 0 ? pre_dest : -1;
+  if (!kSwiglu) {
+    const int prow = row0 + min(tid, mrows - 1);
+    reinterpret_cast<uint64_t*>(smem + kWideTables + 2 * kTileBM * 4)[tid] =
+        pre_on != 0 && pre_dest >= 0 ? reinterpret_cast<uint64_t>(g.y_direct + static_cast<int64_t>(pre_dest) * g.n)
+                                     : reinterpret_cast<uint64_t>(g.c + static_cast<int64_t>(prow) * g.n);
+  }
   lds_barrier();
 #pragma unroll
   for (int gi = 0; gi < kAhead; ++gi) abuf[gi] = read_group(0, gi);
