@@ -27,7 +27,7 @@ namespace {
 constexpr int kSmallThreads = 1024;
 constexpr int kSmallWaves = kSmallThreads / kWave;
 constexpr int kSmallMaxExperts = 256;
-constexpr int kChunkThreads = 256;
+constexpr int kChunkThreads = 1024;
 constexpr int kChunkWaves = kChunkThreads / kWave;
 
 // Assigns rows to one 64-task pass in task order; base[e] is this wave's running base.

@@ -66,6 +66,7 @@ ROUTE_CASES = {
     "ragged": (777, 32, 6, 256),
     "zipf": (3000, 32, 6, "zipf"),
     "wide": (2500, 40, 8, 64),
+    "chunked": (20000, 32, 6, 256),  # 120,000 tasks: count + scatter kernels over 117 chunks
 }
 
 
