@@ -696,7 +696,9 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
 
   // prologue: the epilogue's scales (thread t: row t's A scale, and the weight-row scale of
   // its wave's column lane), A stages 0 and 1 into LDS, stage 2 into register set 0, B steps
-  // 0..3, the first operands. Rows past mrows take the last row's scale (never stored).
+  // 0..3, the first operands; the loads of stages 0, 1 and 2 go out together (stage 0 through
+  // registers of the prologue's own), so that stage 2 is in before the first stage needs it.
+  // Rows past mrows take the last row's scale (never stored).
   const float pre_xs = row_scale<kGather>(g, rs, row0 + min(tid, mrows - 1));
   // GEMM2: row tid's output address (its part row, or its token's y row when the token has no
   // other routed slot and direct rows are on); the switch and the row table load side by side
@@ -706,16 +708,18 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     pre_dest = g.row_dest[row0 + min(tid, mrows - 1)];
   }
   const float pre_bs = g.b_scale[static_cast<int64_t>(e) * g.n + weight_row<kSwiglu>(g, unit, kStreamUnit, lane)];
+  int4 ra0[kALoads];
 #pragma unroll
-  for (int i = 0; i < kALoads; ++i) load_a(0, i, 0);
+  for (int i = 0; i < kALoads; ++i) ra0[i] = ld16(a_src[i]);
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) load_a(1, i, min(1, last_stage));
 #pragma unroll
+  for (int i = 0; i < kALoads; ++i) load_a(0, i, min(2, last_stage));
+#pragma unroll
   for (int sl = 0; sl < kWideRing; ++sl) load_b(sl, min(sl, last_step));
 #pragma unroll
-  for (int i = 0; i < kALoads; ++i) store_a(0, i, 0);
-#pragma unroll
-  for (int i = 0; i < kALoads; ++i) load_a(0, i, min(2, last_stage));
+  for (int i = 0; i < kALoads; ++i)
+    *reinterpret_cast<int4*>(smem + a_dst0 + i * kRowsPerLoad * kWideBK) = ra0[i];  // stage 0, buffer 0
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) store_a(1, i, 1);
   reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
