@@ -42,7 +42,7 @@
 //    SIMD with its 256 accumulators in AGPRs, 256 x 256 tiles, weights straight into
 //    registers and only A through LDS; described at wide_tile.
 #include <algorithm>
-#include <algorithm>
+#include <atomic>
 
 #include "common.cuh"
 #include "kernels.h"
@@ -1075,15 +1075,26 @@ __global__ __launch_bounds__(kWideThreads, 1) void wide_gemm_kernel(GemmArgs g) 
   }
 }
 
+// The dynamic-LDS limit of kernel K raised to `bytes` (above the default) once per device of
+// the process (the attribute is set for the current device; a bit per device id below 64).
+template <auto K>
+hipError_t ensure_dynamic_lds(int bytes) {
+  static std::atomic<uint64_t> done{0};
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (1ull << dev) : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit) != 0) return hipSuccess;
+  err = hipFuncSetAttribute(reinterpret_cast<const void*>(K), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (err == hipSuccess && bit != 0) done.fetch_or(bit, std::memory_order_release);
+  return err;
+}
+
 template <bool kGather, bool kSwiglu>
 hipError_t launch_wide(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
-  static bool attr_set = false;  // the 96 KB of dynamic LDS exceeds the default limit
-  if (!attr_set) {
-    const hipError_t err =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&wide_gemm_kernel<kGather, kSwiglu>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kWideSmemBytes);
+  {  // the 104 KB of dynamic LDS exceeds the default limit
+    const hipError_t err = ensure_dynamic_lds<&wide_gemm_kernel<kGather, kSwiglu>>(kWideSmemBytes);
     if (err != hipSuccess) return err;
-    attr_set = true;
   }
   const int64_t bound =
       (static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * ((g.n + kTileBN - 1) / kTileBN);
@@ -1096,13 +1107,9 @@ hipError_t launch_wide(const GemmArgs& g, int max_rows, int num_cus, hipStream_t
 
 template <bool kGather, bool kSwiglu, bool kAnyK>
 hipError_t launch_engines_k(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
-  static bool attr_set = false;  // the 128 KB of dynamic LDS exceeds the default limit
-  if (!attr_set) {
-    const hipError_t err =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_kernel<kGather, kSwiglu, kAnyK>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes);
+  {  // the 128 KB of dynamic LDS exceeds the default limit
+    const hipError_t err = ensure_dynamic_lds<&grouped_gemm_kernel<kGather, kSwiglu, kAnyK>>(kSmemBytes);
     if (err != hipSuccess) return err;
-    attr_set = true;
   }
   // upper bound of the work items over any split of max_rows rows into the experts
   const int64_t stream_nb = (g.n / kStreamUnit + kGemmWaves - 1) / kGemmWaves;

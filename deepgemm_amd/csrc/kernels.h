@@ -36,7 +36,7 @@ struct RouteArgs {
 hipError_t launch_route(const RouteArgs& a, int64_t max_tasks, hipStream_t stream);
 
 // Per-expert tile engine of the grouped GEMM: kAuto picks STREAM for experts with <= 64 rows
-// (weight streaming, decode) and TILE otherwise (128x128 MFMA tiles, prefill).
+// (weight streaming, decode) and TILE otherwise (256x256 MFMA tiles, prefill).
 enum class GemmEngine : int { kAuto = 0, kStream = 1, kTile = 2 };
 
 // Fused GEMM1 epilogue: SwiGLU x route weight -> fp32 y.

@@ -165,7 +165,9 @@ def get_mega_moe_hip_build_config():
     config["large_opt_3stage_default_threshold"] = _LARGE_OPT_DEFAULT_THRESHOLD
     config["large_opt_3stage_shape"] = "single GPU: experts<=256, topk<=16, H,I % 128 == 0"
     config["large_opt_3stage_selection"] = ("auto: per expert on device (<=64 rows: streaming "
-                                            "engine, else 128x128 MFMA tiles)")
+                                            "engine, else 256x256 MFMA tiles); every GEMM on "
+                                            "the 4-wave 256x256 kernel when S*K > 8192 and "
+                                            ">= 256 rows per expert on average")
     config["cuda_graph_max_tokens_source"] = "requested num_max_tokens_per_rank"
     config["cuda_graph_execution"] = "explicit_big_fused_or_large_opt_3stage"
     return config

@@ -50,7 +50,9 @@ extern "C" {
 
 /* Schedule of mmoe_forward (the reference's MEGAMOE_DCU_USE_LARGE_OPT_3STAGE auto/off/force).
  * The grouped GEMMs have two tile engines; AUTO picks one per expert on the device from its
- * routed row count (<= 64 rows: weight-streaming engine; more: 128x128 MFMA tile engine). */
+ * routed row count (<= 64 rows: weight-streaming engine; more: 256x256 MFMA tile engine). When
+ * every expert has many rows (S*K > 8192 and at least 256 rows per expert on average), AUTO
+ * and STAGED run both GEMMs on a 4-wave 256x256 kernel instead. */
 #define MMOE_SCHEDULE_AUTO 0       /* per-expert choice on the device */
 #define MMOE_SCHEDULE_PERSISTENT 1 /* streaming engine for every expert (HBM-bound decode) */
 #define MMOE_SCHEDULE_STAGED 2     /* tile engine for every expert (MFMA-bound prefill) */
@@ -156,10 +158,14 @@ int mmoe_forward(const mmoe_forward_args* args, void* stream);
 
 /* Stages of mmoe_forward, in order; each reads what the earlier ones left in route_scratch. */
 #define MMOE_STAGE_ROUTE 0   /* counts, offsets, output_index, per-row tables, stats */
-#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I] */
-#define MMOE_STAGE_REQUANT 2 /* row max |y| -> amax [R], act e4m3 [R, I], act_scale [R] */
-#define MMOE_STAGE_GEMM2 3   /* part bf16 [R, H] */
-#define MMOE_STAGE_COMBINE 4 /* y */
+#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I]; on the 4-wave
+                                kernel the bf16 pre-activation h [R, 2I] in y's bytes instead
+                                (meta[1] = 1) */
+#define MMOE_STAGE_REQUANT 2 /* (SwiGLU x weight of h first, when meta[1] = 1) row max |y| ->
+                                amax [R], act e4m3 [R, I], act_scale [R]; row_dest, meta[2] */
+#define MMOE_STAGE_GEMM2 3   /* part bf16 [R, H]; with meta[2] = 1 the rows of single-slot
+                                tokens go straight to y */
+#define MMOE_STAGE_COMBINE 4 /* y (tokens written by GEMM2 are left as they are) */
 
 /* Runs stages [first_stage, last_stage] of mmoe_forward (mmoe_forward = stages 0..4). Lets a
  * profiler bracket each kernel with events and lets tests check each stage on its own. The
