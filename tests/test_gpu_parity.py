@@ -304,6 +304,128 @@ def test_layer_zipf_empty_experts(mm, cuda, full_weights, s):
     assert d <= CALC_DIFF_BAR
 
 
+def _prefill_tokens_gpu(mm, s, global_experts, seed):
+    """Tokens of the prefill configs drawn on the GPU: x ~ N(0,1) cast per token to e4m3;
+    logits N(0,1) [S, global experts] -> softmax -> top-6 -> renormalised, ids outside the 32
+    local experts -> -1."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn((s, 4096), generator=g, device="cuda").to(torch.bfloat16)
+    x_fp8, x_sf = mm.cast_to_fp8_channelwise(x)
+    del x
+    logits = torch.randn((s, global_experts), generator=g, device="cuda")
+    w, idx = torch.topk(torch.softmax(logits, -1), 6, dim=-1)
+    w = (w / w.sum(-1, keepdim=True)).float().contiguous()
+    idx = torch.where(idx < 32, idx, torch.full_like(idx, -1)).to(torch.int64).contiguous()
+    return x_fp8, x_sf, idx, w
+
+
+def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights):
+    """The prefill config c3 at full scale (T = 32768 a rank: 262,144 source tokens, top-6
+    of 256 global experts, experts 0..31 local; ~196K routed rows) through the WIDE
+    kernels. The oracle's whole layer (~10 TFLOP on the host) is out of reach, so the checks
+    are the size-independent ones:
+    - routing bit-exact over all 1.57M tasks;
+    - h, the requant and GEMM2 on a sample of rows (every expert's first and last row, the
+      rows around 256-row tile boundaries, random rows) against the oracle's dequantised
+      matmuls of those rows;
+    - the combine bitwise on sampled tokens with several slots, zero rows for tokens without
+      one, and the direct rows of single-slot tokens equal to their GEMM2 row;
+    - a second call bitwise identical."""
+    l1, l2, l1c, l2c, unpacked = full_weights
+    w1u, w2u = unpacked
+    s = 8 * 32768
+    log(f"prefill full scale S={s}")
+    x_fp8, x_sf, idx, w = _prefill_tokens_gpu(mm, s, 256, seed=1237)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    meta = buf.scratch_view("meta").cpu()
+    assert meta[1].item() == 1 and meta[2].item() == 1, "the WIDE kernels (h, direct rows)"
+
+    # routing, all tasks
+    ref = O.route(idx.cpu(), w.cpu(), 32)
+    r = ref.num_rows
+    log(f"  routed rows {r}")
+    assert meta[0].item() == r
+    assert np.array_equal(buf.scratch_view("counts").cpu().numpy(), ref.counts)
+    assert np.array_equal(buf.scratch_view("offsets").cpu().numpy(), ref.offsets)
+    assert np.array_equal(buf.scratch_view("output_index")[:s].cpu().numpy(), ref.output_index)
+    assert np.array_equal(buf.scratch_view("row_token")[:r].cpu().numpy(), ref.row_token)
+    assert np.array_equal(buf.scratch_view("row_weight")[:r].cpu().numpy(), ref.row_weight)
+
+    # sampled rows
+    gen = np.random.default_rng(5)
+    picks = set()
+    for e in range(32):
+        lo, hi = int(ref.offsets[e]), int(ref.offsets[e + 1])
+        if hi <= lo:
+            continue
+        picks.update({lo, hi - 1})
+        for b in range(lo + 255, hi, 256 * 7):  # tile boundaries (255 | 256) of some blocks
+            picks.update({b, min(b + 1, hi - 1)})
+    picks.update(int(v) for v in gen.integers(0, r, 32))
+    rows = torch.tensor(sorted(picks), dtype=torch.long)
+    tok = torch.from_numpy(ref.row_token)[rows].long()
+    exp = torch.from_numpy(ref.m_indices)[rows].long()
+    xr = x_fp8.view(torch.uint8)[tok.to(cuda)].cpu().view(torch.float8_e4m3fn)
+    xsr = x_sf[tok.to(cuda)].cpu()
+    h = buf.scratch_view("h", r)[rows.to(cuda)].cpu()
+    act = buf.scratch_view("act", r).view(torch.uint8)[rows.to(cuda)].cpu().view(torch.float8_e4m3fn)
+    act_s = buf.scratch_view("act_scale", r)[rows.to(cuda)].cpu()
+    h_ref = torch.empty_like(h)
+    part_ref = torch.empty((rows.numel(), 4096), dtype=torch.bfloat16)
+    for e in exp.unique().tolist():
+        sel = (exp == e).nonzero().view(-1)
+        acc = xr[sel].float() @ w1u[e].float().t()
+        h_ref[sel] = ((acc * xsr[sel].view(-1, 1)) * l1c[1][e].view(1, -1)).to(torch.bfloat16)
+        acc2 = act[sel].float() @ w2u[e].float().t()  # GEMM2 of the GPU's own act rows
+        part_ref[sel] = ((acc2 * act_s[sel].view(-1, 1)) * l2c[1][e].view(1, -1)).to(torch.bfloat16)
+    d_h = O.calc_diff(h.float(), h_ref.float())
+    log(f"  {rows.numel()} sampled rows: calc_diff(h) = {d_h:.2e}")
+    assert d_h < 1e-5, "GEMM1 pre-activation h (sampled rows)"
+    # requant of the GPU's h rows: scales exact from the row max, codes at most one apart
+    y_act = O.swiglu_k2(h, torch.from_numpy(ref.row_weight)[rows], None)
+    amax = y_act.abs().amax(dim=1)
+    assert torch.allclose(buf.scratch_view("amax", r)[rows.to(cuda)].cpu(), amax, rtol=1e-5, atol=0)
+    assert torch.equal(act_s, torch.clamp(buf.scratch_view("amax", r)[rows.to(cuda)].cpu(), min=1e-4) / 448.0)
+    inv = O.fdiv(448.0, torch.clamp(amax, min=1e-4)).view(-1, 1)
+    codes = O.e4m3_from_f32(y_act * inv).view(torch.uint8).to(torch.int16)
+    assert bool(((act.view(torch.uint8).to(torch.int16) - codes).abs() <= 1).all()), "requant codes"
+    # GEMM2 rows: part, or y for a row whose token has a single routed slot
+    row_dest = buf.scratch_view("row_dest", r)[rows.to(cuda)].cpu()
+    part = buf.scratch_view("part", r)[rows.to(cuda)].cpu()
+    direct = row_dest >= 0
+    if bool(direct.any()):
+        part[direct] = y[row_dest[direct].long().to(cuda)].cpu()
+    d_p = O.calc_diff(part.float(), part_ref.float())
+    log(f"  calc_diff(GEMM2 rows) = {d_p:.2e} ({int(direct.sum())} of them direct y rows)")
+    assert d_p < 1e-4, "GEMM2 rows (sampled)"
+
+    # combine on sampled tokens
+    slots = (ref.output_index >= 0).sum(axis=1)
+    tsel = []
+    for want in (0, 2, 3):
+        cand = np.nonzero(slots == want if want < 3 else slots >= want)[0]
+        tsel.extend(int(v) for v in cand[:: max(1, cand.size // 24)][:24])
+    tsel = torch.tensor(sorted(set(tsel)), dtype=torch.long)
+    oi = torch.from_numpy(ref.output_index)[tsel]
+    part_all = buf.scratch_view("part", r)
+    got = y[tsel.to(cuda)].cpu()
+    expect = torch.zeros((tsel.numel(), 4096), dtype=torch.float32)
+    for k in range(6):
+        col = oi[:, k]
+        ok = col >= 0
+        if bool(ok.any()):
+            expect[ok] += part_all[col[ok].long().to(cuda)].cpu().float()
+    expect = expect.to(torch.bfloat16)
+    assert torch.equal(got.view(torch.int16), expect.view(torch.int16)), "combine (sampled tokens)"
+
+    y1 = y.clone()
+    run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2, y=y)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y), "two calls bitwise identical"
+
+
 def test_layer_no_routed_rows(mm, cuda):
     """Every slot invalid -> y == 0 exactly (no partial contributes)."""
     s, e, hdim, inter = 10, 4, 256, 128
