@@ -146,21 +146,43 @@ __device__ __forceinline__ int opaque_tid() {
 // first fetches row row0 + t's A scale and route weight, and the values reach the lanes that
 // need them by shuffles, so the whole epilogue waits for two memory round trips instead of a
 // dependent chain per row.
+// The scales store_tile needs: lane t's row scale (and route weight) of row row0 + t, and the
+// lane's weight-row scales (GEMM2: its column in both 32-column tiles; SwiGLU: its gate and up
+// channel). Loaded ahead (before a tile's last MFMAs) so that the epilogue does not wait.
+struct TileScales {
+  float xs, rw, b0, b1;
+};
+
+template <bool kGather, bool kSwiglu>
+__device__ __forceinline__ TileScales tile_scales(const GemmArgs& g, const RowSrc& rs, int e, int row0,
+                                                  int mrows, int unit) {
+  const int lane = opaque_tid() & (kWave - 1);
+  const int rl = lane & 31;
+  TileScales t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (lane < mrows) {
+    t.xs = row_scale<kGather>(g, rs, row0 + lane);
+    if (kSwiglu) t.rw = rs.weight(row0 + lane);
+  }
+  if (!kSwiglu) {
+    t.b0 = g.b_scale[static_cast<int64_t>(e) * g.n + unit * 64 + rl];
+    t.b1 = g.b_scale[static_cast<int64_t>(e) * g.n + unit * 64 + 32 + rl];
+  } else {
+    const int chan = unit * 32 + rl;
+    t.b0 = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
+    t.b1 = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
+  }
+  return t;
+}
+
 template <bool kGather, bool kSwiglu, int MT>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, const RowSrc& rs,
                                            const v16f (&acc)[MT][2], int e, int row0, int mrows,
-                                           int unit) {
+                                           int unit, const TileScales& sc) {
   const int lane = opaque_tid() & (kWave - 1);
   const int rl = lane & 31, hk = lane >> 5;
-  float m_xs = 0.0f, m_rw = 0.0f;
-  if (lane < mrows) {
-    m_xs = row_scale<kGather>(g, rs, row0 + lane);
-    if (kSwiglu) m_rw = rs.weight(row0 + lane);
-  }
+  const float m_xs = sc.xs, m_rw = sc.rw;
   if (!kSwiglu) {
-    float bs[2];
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) bs[ct] = g.b_scale[static_cast<int64_t>(e) * g.n + unit * 64 + ct * 32 + rl];
+    const float bs[2] = {sc.b0, sc.b1};
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -175,8 +197,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const RowSrc& rs,
       }
   } else {
     const int chan = unit * 32 + rl;
-    const float wsg = g.b_scale[static_cast<int64_t>(e) * g.n + chan];
-    const float wsu = g.b_scale[static_cast<int64_t>(e) * g.n + g.sw.inter + chan];
+    const float wsg = sc.b0, wsu = sc.b1;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -321,6 +342,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
     store_chunk(c + 1);  // its buffer was last read in chunk c - 1, before the last barrier
     lds_barrier();
   }
+  const TileScales sc = tile_scales<kGather, kSwiglu>(g, rs, e, row0, mrows, unit);
   {
     const int c = nchunks - 1;
     for (int j = 0; j + D < spc; j += D) {
@@ -336,7 +358,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
   }
 
   if (!active) return;
-  store_tile<kGather, kSwiglu, MT>(g, rs, acc, e, row0, mrows, unit);
+  store_tile<kGather, kSwiglu, MT>(g, rs, acc, e, row0, mrows, unit, sc);
 }
 
 // ------------------------------------------------------------------ TILE engine
@@ -472,9 +494,10 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   const int wrow = row0 + wm * (TM * 32);
   const int wrows = mrows - wm * (TM * 32);
   store_tile<kGather, kSwiglu, 2>(g, rs, *reinterpret_cast<const v16f(*)[2][2]>(&acc[0]), e, wrow,
-                                  wrows, unit);
+                                  wrows, unit, tile_scales<kGather, kSwiglu>(g, rs, e, wrow, wrows, unit));
   store_tile<kGather, kSwiglu, 2>(g, rs, *reinterpret_cast<const v16f(*)[2][2]>(&acc[2]), e, wrow + 64,
-                                  wrows - 64, unit);
+                                  wrows - 64, unit,
+                                  tile_scales<kGather, kSwiglu>(g, rs, e, wrow + 64, wrows - 64, unit));
 }
 
 // ------------------------------------------------------------------ WIDE engine
