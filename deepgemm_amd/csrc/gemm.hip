@@ -141,14 +141,10 @@ __device__ __forceinline__ int opaque_tid() {
 }
 
 // ------------------------------------------------------------------ epilogue
-// Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
-// the tile (mrows <= 64), 64-column unit `unit` of the output (SwiGLU: 32 channels). Lane t
-// first fetches row row0 + t's A scale and route weight, and the values reach the lanes that
-// need them by shuffles, so the whole epilogue waits for two memory round trips instead of a
-// dependent chain per row.
 // The scales store_tile needs: lane t's row scale (and route weight) of row row0 + t, and the
 // lane's weight-row scales (GEMM2: its column in both 32-column tiles; SwiGLU: its gate and up
-// channel). Loaded ahead (before a tile's last MFMAs) so that the epilogue does not wait.
+// channel). The STREAM engine loads them before a tile's last MFMAs so that the epilogue does
+// not wait on them.
 struct TileScales {
   float xs, rw, b0, b1;
 };
@@ -174,6 +170,9 @@ __device__ __forceinline__ TileScales tile_scales(const GemmArgs& g, const RowSr
   return t;
 }
 
+// Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
+// the tile (mrows <= 64), 64-column unit `unit` of the output (SwiGLU: 32 channels). Row r's
+// scale and route weight reach the lanes that need them from lane r of `sc` by shuffles.
 template <bool kGather, bool kSwiglu, int MT>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, const RowSrc& rs,
                                            const v16f (&acc)[MT][2], int e, int row0, int mrows,
