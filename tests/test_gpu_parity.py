@@ -319,12 +319,35 @@ def _prefill_tokens_gpu(mm, s, global_experts, seed):
     return x_fp8, x_sf, idx, w
 
 
-def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights):
-    """The prefill config c3 at full scale (T = 32768 a rank: 262,144 source tokens, top-6
-    of 256 global experts, experts 0..31 local; ~196K routed rows) through the WIDE
-    kernels. The oracle's whole layer (~10 TFLOP on the host) is out of reach, so the checks
-    are the size-independent ones:
-    - routing bit-exact over all 1.57M tasks;
+def _zipf_tokens_gpu(mm, s, seed):
+    """Tokens of the skew config c4 drawn on the GPU: x as above; the 6 slots of a token drawn
+    i.i.d. (with replacement, so a token can hold one expert twice) from Zipf(1.2) over 28 of
+    the 32 experts, 4 chosen experts left empty; route weights uniform in [0.05, 1.05),
+    normalised."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn((s, 4096), generator=g, device="cuda").to(torch.bfloat16)
+    x_fp8, x_sf = mm.cast_to_fp8_channelwise(x)
+    del x
+    live = torch.randperm(32, generator=g, device="cuda")[4:]
+    p = torch.arange(1, live.numel() + 1, device="cuda", dtype=torch.float64) ** (-1.2)
+    draws = torch.multinomial((p / p.sum()).float(), s * 6, replacement=True, generator=g)
+    idx = live[draws].view(s, 6).to(torch.int64).contiguous()
+    w = torch.rand((s, 6), generator=g, device="cuda") + 0.05
+    w = (w / w.sum(-1, keepdim=True)).float().contiguous()
+    return x_fp8, x_sf, idx, w
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c4"])
+def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights, cfg):
+    """The prefill configs at full scale through the WIDE kernels:
+    - c3: T = 32768 a rank (262,144 source tokens, top-6 of 256 global experts, experts 0..31
+      local; ~196K routed rows);
+    - c4: 8192 tokens, Zipf-skewed slots over 28 local experts (49,152 rows, the hottest
+      expert ~15K of them, so its tiles span several XCDs' item ranges; 4 empty experts;
+      repeated (token, expert) slots).
+    The oracle's whole layer (2.5-10 TFLOP on the host) is out of reach, so the checks are the
+    size-independent ones:
+    - routing bit-exact over all tasks;
     - h, the requant and GEMM2 on a sample of rows (every expert's first and last row, the
       rows around 256-row tile boundaries, random rows) against the oracle's dequantised
       matmuls of those rows;
@@ -333,9 +356,13 @@ def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights):
     - a second call bitwise identical."""
     l1, l2, l1c, l2c, unpacked = full_weights
     w1u, w2u = unpacked
-    s = 8 * 32768
-    log(f"prefill full scale S={s}")
-    x_fp8, x_sf, idx, w = _prefill_tokens_gpu(mm, s, 256, seed=1237)
+    if cfg == "c3":
+        s = 8 * 32768
+        x_fp8, x_sf, idx, w = _prefill_tokens_gpu(mm, s, 256, seed=1237)
+    else:
+        s = 8192
+        x_fp8, x_sf, idx, w = _zipf_tokens_gpu(mm, s, seed=1238)
+    log(f"prefill full scale {cfg} S={s}")
     buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
     y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
     torch.cuda.synchronize()
@@ -352,6 +379,12 @@ def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights):
     assert np.array_equal(buf.scratch_view("output_index")[:s].cpu().numpy(), ref.output_index)
     assert np.array_equal(buf.scratch_view("row_token")[:r].cpu().numpy(), ref.row_token)
     assert np.array_equal(buf.scratch_view("row_weight")[:r].cpu().numpy(), ref.row_weight)
+    if cfg == "c4":  # the skew the config is for
+        tiles = (ref.counts + 255) // 256 * 16  # 256 x 256 tiles an expert
+        assert (ref.counts == 0).sum() == 4
+        assert tiles.max() > 2 * tiles.sum() / 8, "hottest expert over 2+ XCD item ranges"
+        srt = np.sort(idx.cpu().numpy(), axis=1)
+        assert (srt[:, 1:] == srt[:, :-1]).any(), "repeated (token, expert) slots"
 
     # sampled rows
     gen = np.random.default_rng(5)
