@@ -337,15 +337,17 @@ def _zipf_tokens_gpu(mm, s, seed):
     return x_fp8, x_sf, idx, w
 
 
-@pytest.mark.parametrize("cfg", ["c3", "c4"])
+@pytest.mark.parametrize("cfg", ["c2", "c3", "c4"])
 def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights, cfg):
     """The prefill configs at full scale through the WIDE kernels:
+    - c2: T = 4096 a rank (32,768 source tokens, same routing as c3; ~24.7K routed rows, the
+      decode/prefill crossover);
     - c3: T = 32768 a rank (262,144 source tokens, top-6 of 256 global experts, experts 0..31
       local; ~196K routed rows);
     - c4: 8192 tokens, Zipf-skewed slots over 28 local experts (49,152 rows, the hottest
       expert ~15K of them, so its tiles span several XCDs' item ranges; 4 empty experts;
       repeated (token, expert) slots).
-    The oracle's whole layer (2.5-10 TFLOP on the host) is out of reach, so the checks are the
+    The oracle's whole layer (1.2-10 TFLOP on the host) is out of reach, so the checks are the
     size-independent ones:
     - routing bit-exact over all tasks;
     - h, the requant and GEMM2 on a sample of rows (every expert's first and last row, the
@@ -356,9 +358,9 @@ def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights, cfg):
     - a second call bitwise identical."""
     l1, l2, l1c, l2c, unpacked = full_weights
     w1u, w2u = unpacked
-    if cfg == "c3":
-        s = 8 * 32768
-        x_fp8, x_sf, idx, w = _prefill_tokens_gpu(mm, s, 256, seed=1237)
+    if cfg in ("c2", "c3"):
+        s = 8 * (4096 if cfg == "c2" else 32768)
+        x_fp8, x_sf, idx, w = _prefill_tokens_gpu(mm, s, 256, seed=1236 if cfg == "c2" else 1237)
     else:
         s = 8192
         x_fp8, x_sf, idx, w = _zipf_tokens_gpu(mm, s, seed=1238)
