@@ -7,6 +7,7 @@ include/megamoe_hip.h. Usage: ``python -m deepgemm_amd.build`` or ``build()``.
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import shutil
 import subprocess
@@ -17,6 +18,9 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB_NAME = "libmegamoe_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
+# sha256 of the sources and flags the library was built from, written next to it by build()
+HASH_PATH = LIB_PATH + ".srchash"
+HEADER = os.path.join(os.path.dirname(HERE), "include", "megamoe_hip.h")
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -38,6 +42,18 @@ def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+def source_hash() -> str:
+    """sha256 over every kernel source and header (csrc/*.hip, *.cuh, *.h, the C-ABI header)
+    and the compiler flags: a library whose recorded hash differs is stale."""
+    h = hashlib.sha256(" ".join(HIPCC_FLAGS).encode())
+    files = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cuh", ".h")))
+    for path in [os.path.join(CSRC, f) for f in files] + [HEADER]:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
 def _compile(src: str, hipcc: str, verbose: bool) -> str:
     obj = os.path.join(OBJ_DIR, os.path.basename(src) + ".o")
     cmd = [hipcc, *HIPCC_FLAGS, "-c", src, "-o", obj]
@@ -52,6 +68,7 @@ def _compile(src: str, hipcc: str, verbose: bool) -> str:
 def build(verbose: bool = False, jobs: int = 8) -> str:
     """Compile all kernels for gfx950 and link libmegamoe_hip.so; returns its path."""
     hipcc = _hipcc()
+    digest = source_hash()  # of the sources as they are when the compiles start
     os.makedirs(OBJ_DIR, exist_ok=True)
     srcs = sources()
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
@@ -62,6 +79,8 @@ def build(verbose: bool = False, jobs: int = 8) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, LIB_PATH)
+    with open(HASH_PATH, "w") as fh:
+        fh.write(digest + "\n")
     return LIB_PATH
 
 

@@ -49,15 +49,6 @@ def _large_opt_3stage_threshold() -> int:
     return int(os.getenv(_LARGE_OPT_THRESHOLD_ENV, str(_LARGE_OPT_DEFAULT_THRESHOLD)))
 
 
-def _large_opt_3stage_selected(num_tokens: int, mode: str, threshold: int) -> bool:
-    """megamoe/__init__.py:38-43 (strict '>' against the threshold)."""
-    if mode == "force":
-        return True
-    if mode == "auto":
-        return num_tokens > threshold
-    return False
-
-
 def _schedule_for_mode(mode: str) -> int:
     """auto -> per-expert engine choice on the device; force -> tile engine; off -> streaming
     engine (see fp8_mega_moe)."""
@@ -66,6 +57,18 @@ def _schedule_for_mode(mode: str) -> int:
     if mode == "off":
         return _capi.MMOE_SCHEDULE_PERSISTENT
     return _capi.MMOE_SCHEDULE_AUTO
+
+
+def _eager_schedule(mode: str, threshold: int, dispatch_tokens: int) -> int:
+    """Schedule of an eager call. The reference runs its persistent fused kernel for
+    ``dispatch_tokens <= threshold`` in auto mode and the staged K1/K2/K3 path above it
+    (megamoe/__init__.py:38-43, :408-428). Here the persistent counterpart is the streaming
+    engine for every expert (MMOE_SCHEDULE_PERSISTENT); above the threshold auto keeps the
+    per-expert engine choice on the device. ``force`` and ``off`` ignore the threshold, as in
+    the reference."""
+    if mode == "auto" and dispatch_tokens <= threshold:
+        return _capi.MMOE_SCHEDULE_PERSISTENT
+    return _schedule_for_mode(mode)
 
 
 def _is_current_stream_capturing() -> bool:
@@ -179,10 +182,6 @@ def get_token_alignment_for_mega_moe() -> int:
 
 def _group_size(group) -> int:
     return 1 if group is None else int(group.size())
-
-
-def _group_rank(group) -> int:
-    return 0 if group is None else int(group.rank())
 
 
 # ---------------------------------------------------------------------------------------
@@ -561,17 +560,27 @@ def fp8_mega_moe(
     Schedules: the reference's persistent small-T kernel and staged large-T path become two
     tile engines of one persistent grouped GEMM, chosen per expert on the device from its
     routed rows (the row counts exist only there). ``MEGAMOE_DCU_USE_LARGE_OPT_3STAGE``
-    keeps its meaning: ``auto`` (default) = per-expert choice, ``1``/``3stage`` = tile engine
-    everywhere, ``0``/``off`` = streaming engine everywhere; every choice computes the same
-    layer. Flags, ``dispatch_num_tokens`` and graph-mode rules are validated exactly as in the
-    reference. Graph modes read the device token count ``sym_buffer.cuda_graph_num_tokens`` at
+    keeps its meaning: ``auto`` (default) = the streaming engine for every expert when the
+    call's token count is at most ``MEGAMOE_DCU_LARGE_OPT_3STAGE_TOKEN_THRESHOLD`` (default
+    128, the reference's persistent-path rule), else the per-expert choice; ``1``/``3stage`` =
+    tile engine everywhere; ``0``/``off`` = streaming engine everywhere. Every choice computes
+    the same layer, bit for bit. Graph modes use the mode alone (the token count of a replay is
+    only known on the device). Flags, ``dispatch_num_tokens`` and graph-mode rules are
+    validated exactly as in the reference. Graph modes read the device token count ``sym_buffer.cuda_graph_num_tokens`` at
     run time; the launch sequence allocates nothing and never synchronises, so it captures."""
     call_y = y
     if big_fused_cuda_graph and stages_fused_cuda_graph:
         raise ValueError("choose only one of big_fused_cuda_graph or stages_fused_cuda_graph")
     graph_mode = big_fused_cuda_graph or stages_fused_cuda_graph
     mode = getattr(sym_buffer, "_large_opt_3stage_mode", None) or _large_opt_3stage_mode()
+    threshold = getattr(sym_buffer, "_large_opt_3stage_threshold", None)
+    if threshold is None:
+        threshold = _large_opt_3stage_threshold()
     runtime_tokens = None
+    # fast_math=False is refused where the reference refuses it: the staged paths check it
+    # first (megamoe/large_opt.py:381, :526), the persistent kernel after the tensor checks
+    # (csrc/kernels/mega_moe_fused_hip.cu:87-91)
+    persistent_no_fast_math = False
     if graph_mode:
         graph_max_tokens = int(sym_buffer.cuda_graph_max_tokens_per_rank)
         capture_rows = int(y.size(0))
@@ -585,6 +594,9 @@ def fp8_mega_moe(
         if stages_fused_cuda_graph and mode == "off":
             raise RuntimeError("stages_fused_cuda_graph=True requires "
                                "MEGAMOE_DCU_USE_LARGE_OPT_3STAGE=auto or 1")
+        if stages_fused_cuda_graph and not fast_math:
+            raise RuntimeError("large-opt DCU MegaMoE graph path requires fast_math")
+        persistent_no_fast_math = not fast_math
         call_y = y[:graph_max_tokens] if capture_rows != graph_max_tokens else y
         runtime_tokens = sym_buffer.cuda_graph_num_tokens
         schedule = _schedule_for_mode(mode)
@@ -599,11 +611,15 @@ def fp8_mega_moe(
         if dispatch_tokens < 0 or dispatch_tokens > int(sym_buffer.num_max_tokens_per_rank):
             raise ValueError("dispatch_num_tokens must be in "
                              f"0..{int(sym_buffer.num_max_tokens_per_rank)}")
-        schedule = _schedule_for_mode(mode)
-    if not fast_math:  # both reference paths refuse it (mega_moe_fused_hip.cu:87-91, large_opt.py:381)
-        raise RuntimeError("DCU MegaMoE W8A8 channelwise persistent fused path requires fast_math")
+        staged = mode == "force" or (mode == "auto" and dispatch_tokens > threshold)
+        if staged and not fast_math:
+            raise RuntimeError("large-opt DCU MegaMoE path requires fast_math")
+        persistent_no_fast_math = not fast_math
+        schedule = _eager_schedule(mode, threshold, dispatch_tokens)
     _validate_layer_tensors(call_y, l1_weights, l2_weights, cumulative_local_expert_recv_stats,
                             sym_buffer, recipe, activation)
+    if persistent_no_fast_math:
+        raise RuntimeError("DCU MegaMoE W8A8 channelwise persistent fused path requires fast_math")
     _launch_layer(call_y, l1_weights, l2_weights, cumulative_local_expert_recv_stats, sym_buffer,
                   activation_clamp, schedule, runtime_tokens)
 

@@ -118,8 +118,27 @@ def _build_library() -> None:
     _build.build()
 
 
+def check_fresh(path: str = LIB_PATH) -> None:
+    """Raise when the library was built from other sources or flags than those in the tree
+    (the hash build() records next to it differs from the tree's), so that a kernel edit
+    without a rebuild never runs a stale binary."""
+    from .. import build as _build
+
+    if os.path.abspath(path) != os.path.abspath(_build.LIB_PATH):
+        return
+    try:
+        with open(_build.HASH_PATH) as fh:
+            built = fh.read().strip()
+    except OSError:
+        built = None
+    if built != _build.source_hash():
+        raise OSError(f"{path} is stale: it was not built from the kernel sources in this tree "
+                      "(run `python -m deepgemm_amd.build`)")
+
+
 def load(path: str = LIB_PATH, build_if_missing: bool = True):
-    """Load (building once if absent) the gfx950 library and declare every entry point."""
+    """Load (building once if absent) the gfx950 library and declare every entry point.
+    A library that does not match the tree's sources raises (check_fresh)."""
     global _lib
     with _lock:
         if _lib is not None:
@@ -128,6 +147,7 @@ def load(path: str = LIB_PATH, build_if_missing: bool = True):
             if not build_if_missing:
                 raise OSError(f"{path} is missing; run `python -m deepgemm_amd.build`")
             _build_library()
+        check_fresh(path)
         lib = ctypes.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)

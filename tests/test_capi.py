@@ -150,3 +150,14 @@ def test_forward_zero_tokens_is_a_noop():
 def test_check_raises_runtime_error():
     with pytest.raises(RuntimeError, match="too many tokens"):
         _capi.check(-6, "fp8_mega_moe")
+
+
+def test_stale_library_is_refused(monkeypatch):
+    """A library whose recorded source hash differs from the tree's raises instead of loading
+    (a kernel edit without a rebuild must not run the old binary)."""
+    from deepgemm_amd import build as hip_build
+
+    _capi.check_fresh()  # the tree's library is fresh
+    monkeypatch.setattr(hip_build, "source_hash", lambda: "0" * 64)
+    with pytest.raises(OSError, match="stale"):
+        _capi.check_fresh()

@@ -234,21 +234,44 @@ def full_weights(mm):
     return l1, l2, l1c, l2c, unpacked
 
 
-@pytest.mark.parametrize("case", ["c0", "c1_128", "ragged_77", "clamp10", "wide_2048"])
+# case: (S, global experts or "zipf", activation_clamp, GEMM1 kernel: "8wave" or "wide")
+FULL_SHAPE_CASES = {
+    "c0": (64, None, None, "8wave"),
+    "c1_128": (1024, 256, None, "8wave"),
+    "ragged_77": (77, 64, None, "8wave"),
+    "clamp10": (96, None, 10.0, "8wave"),
+    "wide_2048": (2048, None, None, "wide"),
+    # clamp 1.0 binds on both sides of the gate and of the up value (h ~ N(0, 1)): the 8-wave
+    # epilogue on the STREAM engine (c1 routing), on the TILE engine (Zipf: experts with more
+    # than 64 rows), and the WIDE kernel's requant from h
+    "clamp1_stream": (1024, 256, 1.0, "8wave"),
+    "clamp1_tile": (600, "zipf", 1.0, "8wave"),
+    "clamp1_wide": (2048, None, 1.0, "wide"),
+}
+
+
+def _assert_clamp_binds(h: torch.Tensor, clamp: float, min_frac: float = 0.05):
+    """At least min_frac of the gate values lie above +c and below -c, and so do the up values:
+    the clamp changes values on every side it applies to, and gate values below -c (which the
+    one-sided K2 gate clamp leaves alone) are common."""
+    inter = h.shape[1] // 2
+    g, u = h[:, :inter].float(), h[:, inter:].float()
+    fracs = {"gate>c": (g > clamp).float().mean().item(), "gate<-c": (g < -clamp).float().mean().item(),
+             "up>c": (u > clamp).float().mean().item(), "up<-c": (u < -clamp).float().mean().item()}
+    log(f"  clamp {clamp}: fractions beyond it {fracs}")
+    for k, v in fracs.items():
+        assert v >= min_frac, f"clamp does not bind: {k} on {v:.3f} of the values"
+
+
+@pytest.mark.parametrize("case", list(FULL_SHAPE_CASES))
 def test_layer_full_shape(mm, cuda, full_weights, case):
     l1, l2, l1c, l2c, unpacked = full_weights
-    if case == "c0":
-        s, g, clamp = 64, None, None
-    elif case == "c1_128":
-        s, g, clamp = 1024, 256, None
-    elif case == "ragged_77":
-        s, g, clamp = 77, 64, None
-    elif case == "wide_2048":
-        s, g, clamp = 2048, None, None
-    else:
-        s, g, clamp = 96, None, 10.0
+    s, g, clamp, kernel = FULL_SHAPE_CASES[case]
     log(f"layer full-shape case={case} S={s}")
-    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, global_experts=g)
+    if g == "zipf":
+        x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, routing="zipf")
+    else:
+        x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, global_experts=g)
     buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
     stats = torch.zeros(32, dtype=torch.int32, device=cuda)
     y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2, clamp=clamp, stats=stats)
@@ -256,8 +279,12 @@ def test_layer_full_shape(mm, cuda, full_weights, case):
     tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, activation_clamp=clamp,
                             unpacked_weights=unpacked)
     assert np.array_equal(stats.cpu().numpy(), tr.routing.counts)
-    assert (buf.scratch_view("meta")[1].item() == 1) == (case == "wide_2048")
-    assert (buf.scratch_view("meta")[2].item() == 1) == (case == "wide_2048")
+    assert (buf.scratch_view("meta")[1].item() == 1) == (kernel == "wide")
+    assert (buf.scratch_view("meta")[2].item() == 1) == (kernel == "wide")
+    if clamp is not None and clamp < 5.0:
+        _assert_clamp_binds(tr.h, clamp)
+    if g == "zipf":  # the TILE engine: experts with more than 64 rows next to small ones
+        assert (tr.routing.counts > 64).any() and ((tr.routing.counts > 0) & (tr.routing.counts <= 64)).any()
     _stage_checks(buf, tr, s, clamp)
     _combine_bitwise(mm, buf, y, l1, l2, s, clamp)
     d = O.calc_diff(y.cpu(), tr.y)
@@ -553,17 +580,32 @@ def test_deepep_pre_post_process(mm, cuda, ids_dtype):
         assert torch.equal(y.cpu(), acc.to(torch.bfloat16))
 
 
-def test_api_flag_and_tensor_errors(mm, cuda):
+def test_api_flag_and_tensor_errors(mm, cuda, monkeypatch):
     """The reference's flag and tensor checks raise the same exception types and messages
-    (megamoe/__init__.py:343-410, csrc/apis/mega_dcu.hpp:355-433, large_opt.py:381)."""
+    (megamoe/__init__.py:343-410, csrc/apis/mega_dcu.hpp:355-433, large_opt.py:381, :526,
+    mega_moe_fused_hip.cu:87-91), in the same order: the staged paths refuse fast_math=False
+    before any tensor check, the persistent path after them."""
     s, e, hdim, inter, k = 16, 4, 256, 128, 3
     log("api flag/tensor errors")
     x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=5)
     l1, l2 = make_weights_gpu(e, hdim, inter, seed=6, mm=mm)
     buf = mm.SymmBuffer(None, e, s, k, hdim, inter)
     y = torch.empty((s, hdim), dtype=torch.bfloat16, device=cuda)
-    with pytest.raises(RuntimeError, match="requires fast_math"):
+    # 16 tokens <= the default threshold 128: the persistent path
+    with pytest.raises(RuntimeError, match="persistent fused path requires fast_math"):
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf, fast_math=False)
+    with pytest.raises(RuntimeError, match="y must be BF16"):
+        mm.fp8_w8a8_mega_moe(y.float(), l1, l2, buf, fast_math=False)
+    with pytest.raises(RuntimeError, match="persistent fused path requires fast_math"):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, big_fused_cuda_graph=True, fast_math=False)
+    with pytest.raises(RuntimeError, match="large-opt DCU MegaMoE graph path requires fast_math"):
+        mm.fp8_w8a8_mega_moe(y.float(), l1, l2, buf, stages_fused_cuda_graph=True, fast_math=False)
+    # a threshold below the token count: the staged path, refused before the tensor checks
+    monkeypatch.setenv("MEGAMOE_DCU_LARGE_OPT_3STAGE_TOKEN_THRESHOLD", "8")
+    staged_buf = mm.SymmBuffer(None, e, s, k, hdim, inter)
+    with pytest.raises(RuntimeError, match="large-opt DCU MegaMoE path requires fast_math"):
+        mm.fp8_w8a8_mega_moe(y.float(), l1, l2, staged_buf, fast_math=False)
+    monkeypatch.delenv("MEGAMOE_DCU_LARGE_OPT_3STAGE_TOKEN_THRESHOLD")
     with pytest.raises(ValueError, match="choose only one"):
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf, big_fused_cuda_graph=True,
                              stages_fused_cuda_graph=True)

@@ -268,6 +268,55 @@ def test_swiglu_quant_special_rows():
     assert torch.all(qc[3].float() == -448.0)
 
 
+def _k2_scalar(g: float, u: float, w: float, c):
+    """One channel of the staged K2 rule in float64 scalars: the gate is clamped from above
+    only, the up value on both sides (k2_fused_ext.cu:318-327), then g*sigmoid(g)*u*w."""
+    if c is not None:
+        u = min(c, max(-c, u))
+        g = min(c, g)
+    return g / (1.0 + math.exp(-g)) * u * w
+
+
+def test_swiglu_clamp_is_one_sided_on_the_gate():
+    """The K2 clamp (megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:318-327) limits
+    the gate from above only: a gate below -c passes through unclamped. Rows cover a gate
+    below -c, a gate above +c, an up value above +c and below -c, and values inside +-c, each
+    checked against float64 scalars. A two-sided gate clamp (the persistent fused kernel's,
+    mega_moe_dcu_tiles.cuh:540-542) differs materially on the gate < -c entries, so the
+    assertions below tell the two rules apart."""
+    c = 1.0
+    gate = [-3.0, -2.5, -0.5, 0.25, 0.75, 2.0, 4.0, -6.0]
+    up = [0.5, -2.5, 3.0, -0.75, 0.5, -4.0, 1.25, -0.5]
+    inter = len(gate)
+    h = torch.tensor([gate + up], dtype=torch.bfloat16)  # all values exact in bf16
+    w = torch.tensor([0.75])
+    y = O.swiglu_k2(h, w, c)[0].double()
+    want = torch.tensor([_k2_scalar(g, u, 0.75, c) for g, u in zip(gate, up)], dtype=torch.float64)
+    assert torch.allclose(y, want, rtol=2e-6, atol=1e-7)
+    # gate -3 stays -3: y = -3*sigmoid(-3)*0.5*0.75, not -1*sigmoid(-1)*0.5*0.75
+    assert y[0].item() == pytest.approx(-3.0 / (1.0 + math.exp(3.0)) * 0.5 * 0.75, rel=1e-6)
+    two_sided = torch.tensor([_k2_scalar(max(-c, g), u, 0.75, c) for g, u in zip(gate, up)],
+                             dtype=torch.float64)
+    below = torch.tensor([g < -c for g in gate])
+    assert bool(((y - two_sided).abs()[below] > 0.02).all()), "two-sided gate clamp not excluded"
+    assert torch.allclose(y[~below], two_sided[~below], rtol=2e-6, atol=1e-7)
+    # the up clamp is two-sided: up 3.0 -> 1.0 and -4.0 -> -1.0
+    assert y[2].item() == pytest.approx(-0.5 / (1.0 + math.exp(0.5)) * 1.0 * 0.75, rel=1e-6)
+    assert y[5].item() == pytest.approx(1.0 / (1.0 + math.exp(-1.0)) * -1.0 * 0.75, rel=1e-6)
+    # no clamp: every value as given
+    y_none = O.swiglu_k2(h, w, None)[0].double()
+    want_none = torch.tensor([_k2_scalar(g, u, 0.75, None) for g, u in zip(gate, up)],
+                             dtype=torch.float64)
+    assert torch.allclose(y_none, want_none, rtol=2e-6, atol=1e-7)
+    # the requant of the clamped row: scale from its own max |y|, codes from y * 448/a
+    q, s = O.swiglu_quant_k2(h, w, c)
+    amax = float(want.abs().max())
+    assert s[0].item() == pytest.approx(amax / 448.0, rel=1e-6)
+    deq = q[0].float().double() * s[0].double()
+    assert torch.all((deq - want).abs() <= want.abs() * 0.0625 + amax / 448 * 2 ** -9)
+    assert inter == 8
+
+
 def test_swiglu_quant_float64_recompute():
     torch.manual_seed(5)
     h = (torch.randn(64, 256) * 3).to(torch.bfloat16)
