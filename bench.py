@@ -2,17 +2,20 @@
 """Benchmark: one FP8 W8A8 Mega MoE layer (one GPU's expert-parallel share: 32 local experts,
 H=4096, I=2048, top-6) per step, through the drop-in API ``fp8_w8a8_mega_moe``.
 
-Default workload = BASELINE config 1 (decode, HBM-bound): 8x128 = 1024 source tokens routed
-top-6 over 256 global experts from softmax(N(0,1)) logits, only experts 0..31 kept (~768 rows).
-Synthetic seeded data, random-init weights N(0, 1/sqrt(K)) quantised channelwise to e4m3.
+Headline workload (``value``) = BASELINE config 1 (decode, HBM-bound): 8x128 = 1024 source
+tokens routed top-6 over 256 global experts from softmax(N(0,1)) logits, only experts 0..31
+kept (~768 rows). The same run also times configs 2-4 (T=4096 crossover, T=32768 prefill,
+Zipf-skewed T=8192) and reports each under ``per_config``. Synthetic seeded data,
+random-init weights N(0, 1/sqrt(K)) quantised channelwise to e4m3.
 
-Timing: W warm-up layers, then K timed layers. Before every layer a 1 GiB buffer is read (a
-reduction) to flush the L2/MALL outside the timed events -- a read, so no dirty lines are left
-whose write-back would be charged to the layer; each layer is bracketed by HIP events on the
-stream it runs on. A second pass launches the five stages separately with events between them
-to attribute time per kernel (roofline of the dominant kernel). The CPU baseline is the
+Timing: W warm-up layers, then K timed layers per config. Before every layer a 1 GiB buffer is
+read (a reduction) to flush the L2/MALL outside the timed events -- a read, so no dirty lines
+are left whose write-back would be charged to the layer; each layer is bracketed by HIP events
+on the stream it runs on. A second pass launches the stages separately with events between
+them to attribute time per kernel (roofline of the dominant kernel). The CPU baseline is the
 repository's own oracle (a restatement of the reference's dequantise-and-matmul baseline) on
-the host cores, on a bounded sample of the same workload.
+all host cores: the whole c1 layer three times (median), and a bounded sample of each other
+config.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -22,6 +25,7 @@ import argparse
 import json
 import math
 import os
+import platform
 import statistics
 import sys
 import time
@@ -32,6 +36,7 @@ sys.path.insert(0, ROOT)
 E_LOCAL, HIDDEN, INTER, TOPK = 32, 4096, 2048, 6
 HBM_PEAK_BPS = 8.0e12       # MI355X HBM3E
 FP8_PEAK_FLOPS = 5.0e15     # MI355X dense FP8 MFMA
+ROUTE_IN_GEMM1_MAX_TASKS = 8192  # tasks (S*K) up to which GEMM1 routes in-kernel
 
 CONFIGS = {
     "c0": dict(id=0, tokens=64, global_experts=None, routing="softmax",
@@ -45,6 +50,7 @@ CONFIGS = {
     "c4": dict(id=4, tokens=8192, global_experts=None, routing="zipf",
                workload="c4 skew T=8192: top-6 i.i.d. Zipf(1.2) over 28 experts, 4 empty"),
 }
+HEADLINE = "c1"
 
 
 def log(msg: str) -> None:
@@ -83,8 +89,21 @@ def profiled_traffic(config_id: str, kernel: str):
     return None
 
 
-def make_inputs(cfg: dict, torch, mm):
-    """Seeded synthetic inputs drawn on the GPU (seed 1234 + config id)."""
+def make_weights(torch, mm, seed: int):
+    """W1 ~ N(0, 1/sqrt(H)) [E, 2I, H], W2 ~ N(0, 1/sqrt(I)) [E, H, I], drawn on the GPU and
+    transformed by the package (channelwise e4m3 cast + Marlin)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w1 = (torch.randn((E_LOCAL, 2 * INTER, HIDDEN), generator=g, device="cuda")
+          / math.sqrt(HIDDEN)).to(torch.bfloat16)
+    w2 = (torch.randn((E_LOCAL, HIDDEN, INTER), generator=g, device="cuda")
+          / math.sqrt(INTER)).to(torch.bfloat16)
+    l1, l2 = mm.transform_fp8_weights_for_mega_moe(w1, w2)
+    del w1, w2
+    return l1, l2
+
+
+def make_tokens(cfg: dict, torch, mm):
+    """Seeded synthetic tokens and routing drawn on the GPU (seed 1234 + config id)."""
     seed = 1234 + cfg["id"]
     s = cfg["tokens"]
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -105,79 +124,84 @@ def make_inputs(cfg: dict, torch, mm):
         w = w / w.sum(-1, keepdim=True)
         idx = torch.where(idx < E_LOCAL, idx, torch.full_like(idx, -1)).to(torch.int64)
     x_fp8, x_sf = mm.cast_to_fp8_channelwise(x)
-    w1 = (torch.randn((E_LOCAL, 2 * INTER, HIDDEN), generator=g, device="cuda")
-          / math.sqrt(HIDDEN)).to(torch.bfloat16)
-    w2 = (torch.randn((E_LOCAL, HIDDEN, INTER), generator=g, device="cuda")
-          / math.sqrt(INTER)).to(torch.bfloat16)
-    l1, l2 = mm.transform_fp8_weights_for_mega_moe(w1, w2)
-    del w1, w2, x
-    return x_fp8, x_sf, idx.contiguous(), w.float().contiguous(), l1, l2
+    del x
+    return x_fp8, x_sf, idx.contiguous(), w.float().contiguous()
 
 
-def cpu_baseline(x_fp8, x_sf, idx, w, l1, l2, y_gpu, budget_s: float, torch):
-    """Time the oracle (K2-form dequant pipeline) on the host cores on a bounded sample:
-    the experts [0, n) of the same workload (all 32 when it fits the budget)."""
-    from oracle import megamoe_oracle as O
-
-    threads = torch.get_num_threads()
-    xc, sc, ic, wc = x_fp8.cpu(), x_sf.cpu(), idx.cpu(), w.cpu()
-    l1c = (l1[0].cpu(), l1[1].cpu())
-    l2c = (l2[0].cpu(), l2[1].cpu())
-    total_rows = int(((ic >= 0) & (ic < E_LOCAL) & (wc != 0)).sum())
-    n_exp = E_LOCAL
-    # rough cost model from one timed expert, then shrink the sample to the budget
-    t_start = time.perf_counter()
-    ic1 = torch.where(ic < 1, ic, torch.full_like(ic, -1))
-    O.mega_moe_forward(xc, sc, ic1, wc, (l1c[0][:1], l1c[1][:1]), (l2c[0][:1], l2c[1][:1]))
-    per_exp = time.perf_counter() - t_start
-    n_exp = max(1, min(E_LOCAL, int(budget_s / max(per_exp, 1e-3))))
-    icn = torch.where(ic < n_exp, ic, torch.full_like(ic, -1))
-    l1n = (l1c[0][:n_exp].contiguous(), l1c[1][:n_exp].contiguous())
-    l2n = (l2c[0][:n_exp].contiguous(), l2c[1][:n_exp].contiguous())
-    t0 = time.perf_counter()
-    tr = O.mega_moe_forward(xc, sc, icn, wc, l1n, l2n)
-    dt = time.perf_counter() - t0
-    rows = tr.routing.num_rows
-    parity = None
-    if n_exp == E_LOCAL:
-        parity = O.calc_diff(y_gpu.cpu(), tr.y)
-    # scale to a whole layer by FLOPs (rows) -- weights dequant scales with experts, rows with
-    # rows; the sample keeps both proportional to the full layer
-    scale = total_rows / max(rows, 1)
-    us_layer = dt * scale * 1e6
-    return dict(value=round(us_layer, 1), unit="us/layer", cores=threads, kind="port",
-                sample=f"oracle forward (fp32 dequant matmuls, weight dequant included) on "
-                       f"experts 0..{n_exp - 1}: {rows} of {total_rows} routed rows, "
-                       f"{dt:.2f} s, scaled by rows", parity_calc_diff=parity)
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c1", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-budget-s", type=float, default=20.0)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-stage-timing", action="store_true")
-    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
-                    help="after timing, copy a buffer of this many MiB device-to-device once "
-                         "(a known-size kernel that calibrates rocprof byte counters)")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build runs one GPU's expert-parallel share; --gpus must be 1 "
-              "(multi-GPU dispatch/combine is not built)", file=sys.stderr)
-        return 2
+class CpuOracle:
+    """The oracle (K2-form dequantise-and-matmul pipeline) on the host cores, on CPU copies of
+    the weights unpacked from Marlin once (outside the timing)."""
 
-    import torch
+    def __init__(self, l1, l2, torch):
+        from oracle import megamoe_oracle as O
 
-    from deepgemm_amd import megamoe as mm
+        self.O = O
+        self.torch = torch
+        self.l1 = (l1[0].cpu(), l1[1].cpu())
+        self.l2 = (l2[0].cpu(), l2[1].cpu())
+        self.unpacked = (O.marlin_unpack(self.l1[0], 2 * INTER, HIDDEN),
+                         O.marlin_unpack(self.l2[0], HIDDEN, INTER))
 
-    assert torch.cuda.is_available(), "bench.py needs the MI355X"
-    torch.cuda.set_device(0)
-    cfg = CONFIGS[args.config]
-    log(f"config {args.config}: {cfg['workload']}")
-    x_fp8, x_sf, idx, w, l1, l2 = make_inputs(cfg, torch, mm)
+    def run(self, xc, sc, ic, wc, n_exp: int = E_LOCAL):
+        """One oracle layer over experts [0, n_exp) (the other slots masked to -1); returns
+        (seconds, routed rows, trace)."""
+        torch = self.torch
+        if n_exp < E_LOCAL:
+            # only the tokens with a slot in [0, n_exp): the others would add zero rows to the
+            # combine, whose cost grows with tokens rather than with routed rows
+            ic = torch.where(ic < n_exp, ic, torch.full_like(ic, -1))
+            keep = (ic >= 0).any(dim=1)
+            xc, sc, ic, wc = xc[keep], sc[keep], ic[keep], wc[keep]
+            l1 = (self.l1[0][:n_exp], self.l1[1][:n_exp])
+            l2 = (self.l2[0][:n_exp], self.l2[1][:n_exp])
+            unp = (self.unpacked[0][:n_exp], self.unpacked[1][:n_exp])
+        else:
+            l1, l2, unp = self.l1, self.l2, self.unpacked
+        t0 = time.perf_counter()
+        tr = self.O.mega_moe_forward(xc, sc, ic, wc, l1, l2, unpacked_weights=unp)
+        return time.perf_counter() - t0, tr.routing.num_rows, tr
+
+
+def cpu_full_layer(oracle: CpuOracle, inputs, y_gpu, reps: int):
+    """The whole layer `reps` times on the host cores: median (and all reps), plus the parity
+    of the last run against the GPU's output."""
+    xc, sc, ic, wc = (t.cpu() for t in inputs)
+    times, tr = [], None
+    for _ in range(reps):
+        dt, rows, tr = oracle.run(xc, sc, ic, wc)
+        times.append(dt)
+    return dict(median_s=statistics.median(times), reps_s=[round(t, 3) for t in times],
+                rows=rows, parity_calc_diff=oracle.O.calc_diff(y_gpu.cpu(), tr.y))
+
+
+def cpu_sample(oracle: CpuOracle, inputs, total_rows: int, budget_s: float):
+    """A bounded sample of a larger config: the layer over experts [0, n), n chosen from one
+    timed expert to fit the budget, scaled to the whole layer by routed rows."""
+    xc, sc, ic, wc = (t.cpu() for t in inputs)
+    dt1, _, _ = oracle.run(xc, sc, ic, wc, 1)
+    n_exp = max(1, min(E_LOCAL, int(budget_s / max(dt1, 1e-3))))
+    dt, rows, _ = oracle.run(xc, sc, ic, wc, n_exp)
+    return dict(us_per_layer=round(dt * total_rows / max(rows, 1) * 1e6, 1),
+                sample=f"experts 0..{n_exp - 1}: {rows} of {total_rows} routed rows in "
+                       f"{dt:.2f} s, scaled by rows")
+
+
+def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
+    """Times the layer (and its stages) on one config; returns (result dict, inputs, y)."""
+    log(f"config {name}: {cfg['workload']}")
+    inputs = make_tokens(cfg, torch, mm)
+    x_fp8, x_sf, idx, w = inputs
     s = cfg["tokens"]
     buf = mm.get_symm_buffer_for_mega_moe(None, E_LOCAL, s, TOPK, HIDDEN, INTER)
     buf.x[:s].copy_(x_fp8)
@@ -185,29 +209,17 @@ def main() -> int:
     buf.topk_idx[:s].copy_(idx)
     buf.topk_weights[:s].copy_(w)
     y = torch.empty((s, HIDDEN), dtype=torch.bfloat16, device="cuda")
-    # Cache flush between steps: READ 1 GiB (a reduction), which evicts L2/MALL without leaving
-    # dirty lines whose write-back would be charged to the next layer.
-    flush = torch.ones((1 << 28,), dtype=torch.float32, device="cuda")
-
-    def flush_cache():
-        flush.sum()
 
     def layer():
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf)
 
-    log(f"warmup {args.warmup}")
     for _ in range(max(1, args.warmup)):
         layer()
     torch.cuda.synchronize()
     counts = buf.scratch_view("counts").cpu()
     rows = int(counts.sum())
     touched = int((counts > 0).sum())
-    mode = buf._large_opt_3stage_mode
-    schedule = {"auto": "auto (per-expert engine)", "force": "tile engine",
-                "off": "streaming engine"}[mode]
-    stream_experts = int(((counts > 0) & (counts <= 64)).sum())
-    log(f"routed rows R={rows}, touched experts={touched}, schedule={schedule}, "
-        f"experts on the streaming engine={stream_experts if mode == 'auto' else '-'}")
+    log(f"  routed rows R={rows}, touched experts={touched}, largest expert={int(counts.max())}")
 
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
@@ -222,15 +234,16 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     ms = [a.elapsed_time(b) for a, b in zip(starts, ends)]
     med_ms = statistics.median(ms)
-    log(f"layer: median {med_ms * 1e3:.1f} us, min {min(ms) * 1e3:.1f} us")
+    log(f"  layer: median {med_ms * 1e3:.1f} us, min {min(ms) * 1e3:.1f} us")
 
     stage_ms = None
     if not args.no_stage_timing:
-        # The stages as the layer runs them: routing and GEMM1 are one launch when GEMM1 routes
-        # in-kernel (small task counts), so they are timed together; the GEMM1 roofline below
-        # uses that launch.
+        # The stages as the layer runs them: when GEMM1 routes in-kernel (small task counts)
+        # routing and GEMM1 are one launch and are timed together.
         call = mm.LayerCall(y, l1, l2, buf)
-        groups = [("route_gemm1", 0, 1), ("requant", 2, 2), ("gemm2", 3, 3), ("combine", 4, 4)]
+        fused_route = s * TOPK <= ROUTE_IN_GEMM1_MAX_TASKS
+        groups = ([("gemm1", 0, 1)] if fused_route else [("route", 0, 0), ("gemm1", 1, 1)])
+        groups += [("requant", 2, 2), ("gemm2", 3, 3), ("combine", 4, 4)]
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(groups) + 1)]
               for _ in range(args.steps)]
         for i in range(args.steps):
@@ -240,32 +253,26 @@ def main() -> int:
                 call.run(first, last)
                 ev[i][j + 1].record()
         torch.cuda.synchronize()
-        stage_ms = {name: statistics.median(ev[i][j].elapsed_time(ev[i][j + 1])
-                                            for i in range(args.steps))
-                    for j, (name, _, _) in enumerate(groups)}
-        log("stages (median us): " + ", ".join(f"{k}={v * 1e3:.1f}" for k, v in stage_ms.items()))
+        stage_ms = {gname: statistics.median(ev[i][j].elapsed_time(ev[i][j + 1])
+                                             for i in range(args.steps))
+                    for j, (gname, _, _) in enumerate(groups)}
+        log("  stages (median us): " + ", ".join(f"{k}={v * 1e3:.1f}" for k, v in stage_ms.items()))
 
     flops = 6.0 * rows * HIDDEN * INTER
     nbytes = algorithmic_bytes(rows, touched)
     t_s = med_ms * 1e-3
-    tflops = flops / t_s / 1e12
-    hbm_frac = nbytes["layer"] / t_s / HBM_PEAK_BPS
-    mfma_frac = flops / t_s / FP8_PEAK_FLOPS
-    bound = "hbm" if nbytes["layer"] and flops / nbytes["layer"] < FP8_PEAK_FLOPS / HBM_PEAK_BPS \
-        else "mfma"
-
+    bound = "hbm" if flops / max(nbytes["layer"], 1) < FP8_PEAK_FLOPS / HBM_PEAK_BPS else "mfma"
     roofline = None
     if stage_ms is not None:
-        stage_ms["gemm1"] = stage_ms.pop("route_gemm1")
         dom = max(("gemm1", "gemm2"), key=lambda k: stage_ms[k])
         dom_s = stage_ms[dom] * 1e-3
-        prof = profiled_traffic(args.config, dom)
-        traffic = prof[0] if prof else None
+        prof = profiled_traffic(name, dom)
         if bound == "hbm":
             achieved = nbytes[dom] / dom_s / 1e9
             roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1),
                             peak=HBM_PEAK_BPS / 1e9, unit="GB/s",
-                            frac=round(achieved * 1e9 / HBM_PEAK_BPS, 4), traffic=traffic,
+                            frac=round(achieved * 1e9 / HBM_PEAK_BPS, 4),
+                            traffic=prof[0] if prof else None,
                             algorithmic_bytes=nbytes[dom], avg_us=round(stage_ms[dom] * 1e3, 2),
                             traffic_source=prof[1] if prof else None)
         else:
@@ -273,54 +280,146 @@ def main() -> int:
             achieved = kflops / dom_s / 1e12
             roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 1),
                             peak=FP8_PEAK_FLOPS / 1e12, unit="TFLOP/s",
-                            frac=round(achieved * 1e12 / FP8_PEAK_FLOPS, 4), traffic=traffic,
+                            frac=round(achieved * 1e12 / FP8_PEAK_FLOPS, 4),
+                            traffic=prof[0] if prof else None,
                             algorithmic_flops=kflops, avg_us=round(stage_ms[dom] * 1e3, 2),
                             traffic_source=prof[1] if prof else None)
+    res = {
+        "workload": cfg["workload"], "tokens": s, "routed_rows": rows, "touched_experts": touched,
+        "largest_expert_rows": int(counts.max()),
+        "us_median": round(med_ms * 1e3, 2), "us_min": round(min(ms) * 1e3, 2),
+        "fp8_tflops": round(flops / t_s / 1e12, 2),
+        "hbm_frac": round(nbytes["layer"] / t_s / HBM_PEAK_BPS, 4),
+        "mfma_frac": round(flops / t_s / FP8_PEAK_FLOPS, 4),
+        "layer_bound": bound, "algorithmic_bytes": nbytes["layer"], "flops": flops,
+        "stage_us": None if stage_ms is None else {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
+        "roofline": roofline, "wall_s_timed_loop_incl_flush": round(wall, 4),
+    }
+    del buf
+    return res, inputs, y
 
-    cpu = None
+
+def calibrate(torch, mib: int) -> dict:
+    """Two known-size kernels for the rocprof byte counters of a profiling run: a read of
+    `mib` MiB (a reduction: FETCH = mib MiB) and a device-to-device copy of `mib` MiB
+    (FETCH = WRITE = mib MiB)."""
+    n = mib << 20
+    src = torch.ones((n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    src.view(torch.float32).sum()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"read_bytes": n, "copy_bytes": n}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="c1,c2,c3,c4",
+                    help="configs to time, comma-separated; the headline value is c1's (or the "
+                         "first one's when c1 is not among them)")
+    ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
+                    help="time this one config only (same as --configs NAME)")
+    ap.add_argument("--cpu-reps", type=int, default=3, help="CPU baseline reps of the c1 layer")
+    ap.add_argument("--cpu-sample-s", type=float, default=8.0,
+                    help="CPU seconds of the bounded oracle sample of each other config")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-stage-timing", action="store_true")
+    ap.add_argument("--calibrate-mib", type=int, default=0,
+                    help="after timing, read and copy a buffer of this many MiB once (known-size "
+                         "kernels that calibrate rocprof byte counters)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs one GPU's expert-parallel share on one GPU; --gpus "
+              "must be 1 (every GPU box here has one GPU, and the multi-GPU dispatch/combine "
+              "is not built)", file=sys.stderr)
+        return 2
+    names = [args.config] if args.config else [c.strip() for c in args.configs.split(",") if c.strip()]
+    for n in names:
+        if n not in CONFIGS:
+            ap.error(f"unknown config {n}")
+    headline = HEADLINE if HEADLINE in names else names[0]
+
+    import torch
+
+    from deepgemm_amd import megamoe as mm
+
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    torch.cuda.set_device(0)
+    # Cache flush between steps: READ 1 GiB (a reduction), which evicts L2/MALL without leaving
+    # dirty lines whose write-back would be charged to the next layer.
+    flush = torch.ones((1 << 28,), dtype=torch.float32, device="cuda")
+
+    def flush_cache():
+        flush.sum()
+
+    log("weights: drawing and transforming on the GPU")
+    l1, l2 = make_weights(torch, mm, seed=1234 + CONFIGS[headline]["id"])
+    oracle = None
     if not args.no_cpu_baseline:
-        log("cpu baseline (oracle on host cores)")
-        cpu = cpu_baseline(x_fp8, x_sf, idx, w, l1, l2, y, args.cpu_budget_s, torch)
-        log(f"cpu baseline: {cpu['value']} us/layer on {cpu['cores']} threads; "
-            f"parity calc_diff={cpu.get('parity_calc_diff')}")
+        torch.set_num_threads(os.cpu_count() or 1)
+        oracle = CpuOracle(l1, l2, torch)
+    per_config, cpu = {}, None
+    for name in names:
+        res, inputs, y = time_config(name, CONFIGS[name], l1, l2, args, torch, mm, flush_cache)
+        if oracle is not None:
+            if name == headline:
+                log(f"  cpu baseline: the whole layer x{args.cpu_reps} on "
+                    f"{torch.get_num_threads()} threads")
+                full = cpu_full_layer(oracle, inputs, y, args.cpu_reps)
+                cpu = dict(value=round(full["median_s"] * 1e6, 1), unit="us/layer",
+                           cores=torch.get_num_threads(), kind="port",
+                           sample=f"whole {name} layer ({full['rows']} routed rows), oracle "
+                                  f"dequantise-and-matmul pipeline (K2 form) from FP8 inputs and "
+                                  f"weights, median of {args.cpu_reps} reps {full['reps_s']} s",
+                           os_cpu_count=os.cpu_count(), torch_threads=torch.get_num_threads(),
+                           cpu_model=cpu_model(), parity_calc_diff=full["parity_calc_diff"])
+                res["cpu_us"] = cpu["value"]
+                log(f"  cpu baseline: {cpu['value']} us/layer; parity calc_diff="
+                    f"{full['parity_calc_diff']:.2e}")
+            else:
+                smp = cpu_sample(oracle, inputs, res["routed_rows"], args.cpu_sample_s)
+                res["cpu_us"] = smp["us_per_layer"]
+                res["cpu_sample"] = smp["sample"]
+                log(f"  cpu sample: {smp['us_per_layer']} us/layer ({smp['sample']})")
+        per_config[name] = res
+        del inputs, y
+        torch.cuda.empty_cache()
 
+    h = per_config[headline]
     out = {
         "metric": "us per MoE layer (FP8 W8A8 Mega MoE, one GPU's EP share)",
-        "value": round(med_ms * 1e3, 2),
+        "value": h["us_median"],
         "unit": "us/layer",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(med_ms, 4),
+        "ms_per_step": round(h["us_median"] / 1e3, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8_e4m3 (fp32 accumulate, bf16 out)",
         "data": "synthetic (seeded N(0,1) tokens/logits, N(0,1/sqrt(K)) weights)",
-        "config": {"workload": cfg["workload"], "config_id": args.config, "tokens": s,
+        "config": {"workload": h["workload"], "config_id": headline, "tokens": h["tokens"],
                    "experts": E_LOCAL, "hidden": HIDDEN, "intermediate": INTER, "topk": TOPK,
-                   "routed_rows": rows, "touched_experts": touched, "schedule": schedule},
-        "min_us": round(min(ms) * 1e3, 2),
-        "fp8_tflops": round(tflops, 2),
-        "hbm_frac": round(hbm_frac, 4),
-        "mfma_frac": round(mfma_frac, 4),
-        "layer_bound": bound,
-        "algorithmic_bytes": nbytes["layer"],
-        "flops": flops,
-        "stage_us": None if stage_ms is None else {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
-        "wall_s_timed_loop_incl_flush": round(wall, 4),
-        "flush": "1 GiB read (reduction) before every step, outside the timed events",
-        "roofline": roofline,
+                   "routed_rows": h["routed_rows"], "touched_experts": h["touched_experts"],
+                   "schedule": "auto (per-expert engine)"},
+        "min_us": h["us_min"],
+        "fp8_tflops": h["fp8_tflops"],
+        "hbm_frac": h["hbm_frac"],
+        "mfma_frac": h["mfma_frac"],
+        "layer_bound": h["layer_bound"],
+        "stage_us": h["stage_us"],
+        "roofline": h["roofline"],
         "cpu_baseline": cpu,
+        "per_config": per_config,
+        "flush": "1 GiB read (reduction) before every step, outside the timed events",
     }
-    if args.calibrate_copy_mib > 0:
-        n = args.calibrate_copy_mib << 20
-        src = torch.ones((n,), dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        out["calibration_copy_bytes"] = n
+    if args.calibrate_mib > 0:
+        out["calibration"] = calibrate(torch, args.calibrate_mib)
     print(json.dumps(out), flush=True)
     return 0
 
