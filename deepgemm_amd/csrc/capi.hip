@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "../../include/megamoe_hip.h"
 #include "kernels.h"
@@ -160,6 +161,35 @@ mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratc
   return r;
 }
 
+// ---- scratch of the allocation-free entry point (mmoe_forward_static) ----
+// A file-scope device array: each GPU the library runs on holds its own copy, at its own
+// address, from the code object's load until the process ends. In host code `scratch` is a
+// host-side stand-in, never a device address: the device address comes from
+// hipGetSymbolAddress, once per device, and only that pointer reaches kernels.
+static __device__ __align__(256) uint8_t scratch[MMOE_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_static_scratch[kMaxDevices];
+std::mutex g_static_scratch_mu;
+
+// The current device's address of `scratch` (set up on the first call on that device).
+int static_scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MMOE_ERR_NO_DEVICE;
+  void* p = g_static_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_static_scratch_mu);
+    p = g_static_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+        return MMOE_ERR_HIP;
+      g_static_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return MMOE_OK;
+}
+
 int run_route(const mmoe_forward_args* a, const mmoe_scratch_layout& l, hipStream_t s) {
   const mmoe::RouteArgs r = forward_route_args(a, l);
   const int64_t tasks = static_cast<int64_t>(a->num_tokens) * a->num_topk;
@@ -235,6 +265,9 @@ const char* mmoe_status_string(int status) {
     case MMOE_ERR_HIP: return "HIP kernel launch failed";
     case MMOE_ERR_NO_DEVICE: return "no usable HIP device";
     case MMOE_ERR_ARGUMENT: return "invalid argument";
+    case MMOE_ERR_STATIC_SCRATCH:
+      return "mmoe_forward_static: the call needs more scratch than the static buffer's "
+             "MMOE_STATIC_SCRATCH_BYTES (128 MiB); call mmoe_forward with a route_scratch";
     default: return "unknown status";
   }
 }
@@ -372,6 +405,26 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
 
 int mmoe_forward(const mmoe_forward_args* a, void* stream) {
   return mmoe_forward_stages(a, MMOE_STAGE_ROUTE, MMOE_STAGE_COMBINE, stream);
+}
+
+int mmoe_forward_static(const mmoe_forward_args* args, void* stream) {
+  if (args == nullptr) return MMOE_ERR_NULL_POINTER;
+  mmoe_forward_args a = *args;
+  const int st = check_common(1, a.num_experts, a.num_max_tokens, a.num_topk, a.hidden,
+                              a.intermediate);
+  if (st != MMOE_OK) return st;
+  mmoe_scratch_layout l;
+  plan_scratch(1, a.num_experts, a.num_max_tokens, a.num_topk, a.hidden, a.intermediate, &l);
+  if (l.total_bytes > MMOE_STATIC_SCRATCH_BYTES) return MMOE_ERR_STATIC_SCRATCH;
+  // the same launch sequence as mmoe_forward, on the static scratch of this device: nothing
+  // is allocated, and no kernel of the layer needs zeroed scratch (every table it reads was
+  // written earlier in the same call)
+  void* p = nullptr;
+  const int sst = static_scratch_address(&p);
+  if (sst != MMOE_OK) return sst;
+  a.route_scratch = p;
+  a.route_scratch_bytes = MMOE_STATIC_SCRATCH_BYTES;
+  return mmoe_forward_stages(&a, MMOE_STAGE_ROUTE, MMOE_STAGE_COMBINE, stream);
 }
 
 int mmoe_deepep_preprocess_workspace_bytes(int recv_rows, int topk, int num_experts,

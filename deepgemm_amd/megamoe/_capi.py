@@ -13,6 +13,8 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(_PKG_DIR, "libmegamoe_hip.so")
 
 MMOE_OK = 0
+MMOE_ERR_STATIC_SCRATCH = -15
+MMOE_STATIC_SCRATCH_BYTES = 128 << 20
 MMOE_SCHEDULE_AUTO = 0
 MMOE_SCHEDULE_PERSISTENT = 1
 MMOE_SCHEDULE_STAGED = 2
@@ -93,6 +95,7 @@ SIGNATURES = {
     "mmoe_build_config": (ctypes.c_char_p, []),
     "mmoe_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mmoe_forward": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
+    "mmoe_forward_static": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
     "mmoe_route": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
     "mmoe_forward_stages": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), ctypes.c_int,
                                            ctypes.c_int, c_p]),

@@ -47,6 +47,7 @@ extern "C" {
 #define MMOE_ERR_HIP (-12)               /* a HIP runtime call failed (launch error) */
 #define MMOE_ERR_NO_DEVICE (-13)         /* no usable HIP device / not gfx950 */
 #define MMOE_ERR_ARGUMENT (-14)          /* other invalid argument */
+#define MMOE_ERR_STATIC_SCRATCH (-15)    /* mmoe_forward_static: call exceeds the static scratch */
 
 /* Schedule of mmoe_forward (the reference's MEGAMOE_DCU_USE_LARGE_OPT_3STAGE auto/off/force).
  * The grouped GEMMs have two tile engines; AUTO picks one per expert on the device from its
@@ -155,6 +156,20 @@ const char* mmoe_status_string(int status);
  * path megamoe/large_opt.py:367-508. Routing -> GEMM1 with fused SwiGLU -> requant -> GEMM2
  * -> combine. */
 int mmoe_forward(const mmoe_forward_args* args, void* stream);
+
+/* Allocation-free variant of mmoe_forward. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The caller passes inputs and outputs as for mmoe_forward;
+ * args->route_scratch and args->route_scratch_bytes are ignored. The scratch is instead a
+ * static device array of MMOE_STATIC_SCRATCH_BYTES that the library holds on each GPU it runs
+ * on until the process ends: calls whose mmoe_route_scratch_bytes() (for their num_max_tokens)
+ * exceeds it return MMOE_ERR_STATIC_SCRATCH (128 MiB covers a token capacity of 1152 at
+ * E = 32, H = 4096, I = 2048, top-6). Nothing is allocated on any call (no hipMalloc, no
+ * hipFree, no allocating library routine). Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other host threads) race and must be
+ * serialised by the caller. Results are bitwise those of mmoe_forward. */
+#define MMOE_STATIC_SCRATCH_BYTES (128ll << 20)
+int mmoe_forward_static(const mmoe_forward_args* args, void* stream);
 
 /* Stages of mmoe_forward, in order; each reads what the earlier ones left in route_scratch. */
 #define MMOE_STAGE_ROUTE 0   /* counts, offsets, output_index, per-row tables, stats */
