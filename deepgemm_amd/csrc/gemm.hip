@@ -559,9 +559,9 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
                          : unit * 64 + piece * 8;
   uint16_t* out = (kGemm1 ? reinterpret_cast<uint16_t*>(g.sw.y) : g.c) + static_cast<int64_t>(row0) * ld + col;
 #pragma unroll
-  for (int pass = 0; pass < TM / 2; ++pass) {
+  for (int pass = 0; pass < (TM + 1) / 2; ++pass) {
 #pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
+    for (int t2 = 0; t2 < (TM > 1 ? 2 : 1); ++t2) {  // TM = 1: one row tile, rows 32-63 unused
       const int tm = pass * 2 + t2;
       const float xs = s_xs[tm * 32 + rl];
       const int r = t2 * 32 + rl;  // row within the pass
@@ -606,8 +606,8 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
   }
 }
 
-// TM row tiles of 32: 8 for a full tile, 4 for an expert's last tile of at most 128 rows (half
-// the MFMAs and A traffic for the row remainder).
+// TM row tiles of 32: 8 for a full tile; 4, 2 or 1 for an expert's last tile of at most 128,
+// 64 or 32 rows (a fraction of the MFMAs and A traffic for the row remainder).
 template <bool kGather, bool kSwiglu, int TM>
 __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
                           uint8_t* smem) {
@@ -679,7 +679,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   // stage's first operands, whose buffer is complete since the previous barrier), which
   // covers the LDS latency with one wave per SIMD. Order pinned by sched_barrier.
   constexpr int kGroups = (kWideBK / 64) * TM;
-  constexpr int kAhead = 3;
+  constexpr int kAhead = kGroups >= 4 ? 3 : kGroups - 1;  // TM = 1: two groups a stage
   static_assert(kGroups % (kAhead + 1) == 0, "operand ring index must repeat per stage");
   v8i abuf[kAhead + 1];
   auto read_group = [&](int kt, int gi) {
@@ -914,6 +914,29 @@ __device__ __forceinline__ int expert_of_item(const int* s_prefix, int E, int t)
   return below - 1;
 }
 
+// The items of one workgroup. Workgroup b runs on XCD b % 8, so items are dealt to the XCDs
+// in contiguous ranges and the workgroups of an XCD share its L2 for the same experts' rows and
+// weights (when the grid is not a multiple of 8: one range, the whole grid). A range is dealt
+// in rounds of `step` items (its workgroups); in round k the workgroup takes position
+// (slot + k) % step. The rotation hands every workgroup every position in turn, so items of
+// unequal cost that recur with a period dividing the step (an expert's short last row block)
+// spread over all the workgroups instead of landing on the same few; a round is still the same
+// set of consecutive items, and each round is a bijection, so every item runs exactly once.
+struct ItemDeal {
+  int begin, end, step, slot;
+  __device__ __forceinline__ int rounds() const { return (end - begin + step - 1) / step; }
+  __device__ __forceinline__ int item(int k) const { return begin + k * step + (slot + k) % step; }
+};
+
+__device__ __forceinline__ ItemDeal deal_items(int total) {
+  const int nwg = static_cast<int>(gridDim.x);
+  const int b = static_cast<int>(blockIdx.x);
+  if (nwg % 8 != 0) return ItemDeal{0, total, nwg, b};
+  const int xcd = b % 8;
+  return ItemDeal{static_cast<int>(static_cast<int64_t>(total) * xcd / 8),
+                  static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8), nwg / 8, b / 8};
+}
+
 // TILE item `local` of an expert with cnt rows -> (row block mt, column block nb): row blocks
 // in groups of 4, columns inside a group, so that the consecutive items an XCD runs together
 // form 4 x 8 tiles sharing A rows and B columns in its L2.
@@ -1005,17 +1028,15 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
   const bool fast1 = !kAnyK || g.k % (kAChunk / 32) == 0;
   const bool fast2 = !kAnyK || g.k % (kAChunk / 64) == 0;
-  // Items are dealt to the XCDs in contiguous ranges (workgroup b runs on XCD b % 8), so the
-  // workgroups of an XCD share its L2 for the same experts' A rows.
-  const int nwg = gridDim.x;
-  const bool by_xcd = nwg % 8 == 0;
-  const int xcd = blockIdx.x % 8;
-  const int first = by_xcd ? static_cast<int>(static_cast<int64_t>(total) * xcd / 8) + blockIdx.x / 8
-                           : static_cast<int>(blockIdx.x);
-  const int last = by_xcd ? static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8) : total;
-  const int step = by_xcd ? nwg / 8 : nwg;
-  const float* task_w = reinterpret_cast<const float*>(smem);  // valid until the first item's loads
-  for (int t = first; t < last; t += step) {
+  const ItemDeal deal = deal_items(total);
+  // the route weights cached in LDS are valid until the first item's loads overwrite them
+  const float* task_w = reinterpret_cast<const float*>(smem);
+  bool first_item = true;
+  for (int k = 0; k < deal.rounds(); ++k) {
+    const int t = deal.item(k);
+    if (t >= deal.end) continue;  // the last round's short tail (uniform in the workgroup)
+    const float* item_task_w = first_item ? task_w : nullptr;
+    first_item = false;
     const int e = expert_of_item(s_prefix, E, t);
     const int local = t - s_prefix[e];
     const int cnt = s_count[e];
@@ -1026,7 +1047,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
         const int r0 = mt * kTileBM;
-        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, t == first ? task_w : nullptr, r0,
+        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, item_task_w, r0,
                    nb == 0 ? r0 : 0, nb == 0 ? r0 + kTileBM : 0, 0, 0, s_task, s_tok, s_rw);
         rs = RowSrc{s_tok, s_rw, off_e + r0};
       }
@@ -1040,7 +1061,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
         const int r0 = mc * kStreamRows;
-        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, t == first ? task_w : nullptr, r0,
+        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, item_task_w, r0,
                    nb == 0 ? r0 : 0, nb == 0 ? r0 + kStreamRows : 0, 0, 0, s_task, s_tok, s_rw);
         rs = RowSrc{s_tok, s_rw, row0};
       }
@@ -1075,24 +1096,25 @@ __global__ __launch_bounds__(kWideThreads, 1) void wide_gemm_kernel(GemmArgs g) 
   __syncthreads();
   const int total = s_prefix[E];
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
-  const int nwg = gridDim.x;
-  const bool by_xcd = nwg % 8 == 0;
-  const int xcd = blockIdx.x % 8;
-  const int first = by_xcd ? static_cast<int>(static_cast<int64_t>(total) * xcd / 8) + blockIdx.x / 8
-                           : static_cast<int>(blockIdx.x);
-  const int last = by_xcd ? static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8) : total;
-  const int step = by_xcd ? nwg / 8 : nwg;
+  const ItemDeal deal = deal_items(total);
   const RowSrc rs{g.row_token, g.sw.row_weight, 0};
-  for (int t = first; t < last; t += step) {
+  for (int k = 0; k < deal.rounds(); ++k) {
+    const int t = deal.item(k);
+    if (t >= deal.end) continue;  // the last round's short tail (uniform in the workgroup)
     const int e = expert_of_item(s_prefix, E, t);
     const int cnt = s_count[e];
     int mt, nb;
     tile_coords(t - s_prefix[e], cnt, tile_nb, mt, nb);
     const int mrows = min(kTileBM, cnt - mt * kTileBM);
-    if (mrows > kTileBM / 2)
-      wide_tile<kGather, kSwiglu, kTileBM / 32>(g, rs, e, s_off[e] + mt * kTileBM, mrows, nb, smem);
+    const int row0 = s_off[e] + mt * kTileBM;
+    if (mrows > 128)
+      wide_tile<kGather, kSwiglu, 8>(g, rs, e, row0, mrows, nb, smem);
+    else if (mrows > 64)
+      wide_tile<kGather, kSwiglu, 4>(g, rs, e, row0, mrows, nb, smem);
+    else if (mrows > 32)
+      wide_tile<kGather, kSwiglu, 2>(g, rs, e, row0, mrows, nb, smem);
     else
-      wide_tile<kGather, kSwiglu, kTileBM / 64>(g, rs, e, s_off[e] + mt * kTileBM, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, 1>(g, rs, e, row0, mrows, nb, smem);
     __syncthreads();
   }
 }

@@ -29,6 +29,8 @@ constexpr int kSmallWaves = kSmallThreads / kWave;
 constexpr int kSmallMaxExperts = 256;
 constexpr int kChunkThreads = 1024;
 constexpr int kChunkWaves = kChunkThreads / kWave;
+static_assert(kMaxExperts <= kChunkThreads, "the chunk-count reduction needs a thread per expert");
+static_assert(2 * kChunkThreads <= kChunkWaves * kMaxExperts, "partial sums fit in s_wbase");
 
 // Assigns rows to one 64-task pass in task order; base[e] is this wave's running base.
 __device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t task, bool in_range,
@@ -164,26 +166,37 @@ __global__ __launch_bounds__(kChunkThreads) void route_chunk_scatter_kernel(Rout
   const int wave = tid / kWave;
   const int E = a.num_experts;
   const int chunk = blockIdx.x;
-  // totals and this chunk's base per expert, from every chunk's counts
-  for (int e = tid; e < E; e += kChunkThreads) {
-    int tot0 = 0, tot1 = 0, base = 0;
-    int c = 0;
-    for (; c + 1 < num_chunks; c += 2) {
-      const int v0 = a.chunk_counts[static_cast<int64_t>(c) * E + e];
-      const int v1 = a.chunk_counts[static_cast<int64_t>(c + 1) * E + e];
-      tot0 += v0;
-      tot1 += v1;
-      base += (c < chunk ? v0 : 0) + (c + 1 < chunk ? v1 : 0);
+  // Totals and this chunk's base per expert, from every chunk's counts. Thread t sums the
+  // chunks g, g + G, g + 2G, ... of expert e = t % E (g = t / E, G = 1024 / E groups), so all
+  // threads load at once (consecutive threads, consecutive experts of a chunk row); the G
+  // partial sums of an expert then meet in LDS (s_wbase as scratch, before its own use).
+  {
+    const int groups = kChunkThreads / E;  // >= 1: E <= kMaxExperts == kChunkThreads
+    int* s_ptot = &s_wbase[0][0];
+    int* s_pbase = s_ptot + groups * E;   // 2 * groups * E <= 2 * 1024 ints of s_wbase
+    if (tid < groups * E) {
+      const int e = tid % E, g = tid / E;
+      int tot = 0, base = 0;
+      for (int c = g; c < num_chunks; c += groups) {
+        const int v = a.chunk_counts[static_cast<int64_t>(c) * E + e];
+        tot += v;
+        base += c < chunk ? v : 0;
+      }
+      s_ptot[g * E + e] = tot;
+      s_pbase[g * E + e] = base;
     }
-    if (c < num_chunks) {
-      const int v0 = a.chunk_counts[static_cast<int64_t>(c) * E + e];
-      tot0 += v0;
-      base += c < chunk ? v0 : 0;
+    __syncthreads();
+    for (int e = tid; e < E; e += kChunkThreads) {
+      int tot = 0, base = 0;
+      for (int g = 0; g < groups; ++g) {
+        tot += s_ptot[g * E + e];
+        base += s_pbase[g * E + e];
+      }
+      s_tot[e] = tot;
+      s_cbase[e] = base;
     }
-    s_tot[e] = tot0 + tot1;
-    s_cbase[e] = base;
+    __syncthreads();
   }
-  __syncthreads();
   publish_offsets(a, s_tot, s_off, chunk == 0);
   const int64_t ntasks =
       static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
