@@ -70,8 +70,8 @@ def algorithmic_bytes(rows: int, touched: int) -> dict:
 
 # kernel names as rocprofv3 reports them: the 8-wave persistent kernel (decode-sized configs)
 # or the 4-wave WIDE kernel (many rows per expert)
-PROFILE_KERNELS = {"gemm1": ("grouped_gemm_kernel<true, true, false>", "wide_gemm_kernel<true, true>"),
-                   "gemm2": ("grouped_gemm_kernel<false, false, false>", "wide_gemm_kernel<false, false>")}
+PROFILE_KERNELS = {"gemm1": ("grouped_gemm_kernel<true, true, false>", "wide_gemm_kernel<true, true, 256>"),
+                   "gemm2": ("grouped_gemm_kernel<false, false, false>", "wide_gemm_kernel<false, false, 256>")}
 
 
 def profiled_traffic(config_id: str, kernel: str):

@@ -141,23 +141,35 @@ __device__ __forceinline__ int opaque_tid() {
 }
 
 // ------------------------------------------------------------------ epilogue
-// The scales store_tile needs: lane t's row scale (and route weight) of row row0 + t, and the
-// lane's weight-row scales (GEMM2: its column in both 32-column tiles; SwiGLU: its gate and up
-// channel). The STREAM engine loads them before a tile's last MFMAs so that the epilogue does
-// not wait on them.
-struct TileScales {
+// Per-tile scales: row r's A scale (its token's, when gathering) and route weight (SwiGLU), and
+// each lane's weight-row scales (GEMM2: its column in both 32-column tiles; SwiGLU: its gate and
+// up channel). They are loaded into registers at the start of an item and written into a static
+// LDS table just before the barrier that completes the item's first A chunk (or stage): the A
+// loads issued after them have landed by then, so that costs no wait of its own, and the
+// epilogue reads LDS instead of memory. (Loaded before a tile's last MFMAs instead, the compiler
+// sank the loads into the epilogue: a memory round trip after the last MFMA, then a full vmcnt
+// wait behind the first output stores.)
+struct TileTables {
+  float xs[kTileBM];               // row scale of tile row r
+  float rw[kTileBM];               // route weight of tile row r (SwiGLU)
+  float bs[kGemmWaves][2][kWave];  // wave w, lane l: its two weight-row scales
+};
+
+struct TileScaleRegs {
   float xs, rw, b0, b1;
 };
 
+// Thread t: tile row t's scales (t < mrows <= 512 threads), and its lane's weight-row scales of
+// the 64-column unit `unit` (a valid unit).
 template <bool kGather, bool kSwiglu>
-__device__ __forceinline__ TileScales tile_scales(const GemmArgs& g, const RowSrc& rs, int e, int row0,
-                                                  int mrows, int unit) {
-  const int lane = opaque_tid() & (kWave - 1);
-  const int rl = lane & 31;
-  TileScales t{0.0f, 0.0f, 0.0f, 0.0f};
-  if (lane < mrows) {
-    t.xs = row_scale<kGather>(g, rs, row0 + lane);
-    if (kSwiglu) t.rw = rs.weight(row0 + lane);
+__device__ __forceinline__ TileScaleRegs load_tile_scales(const GemmArgs& g, const RowSrc& rs, int e,
+                                                          int row0, int mrows, int unit) {
+  const int tid = opaque_tid();
+  const int rl = tid & 31;
+  TileScaleRegs t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (tid < mrows) {
+    t.xs = row_scale<kGather>(g, rs, row0 + tid);
+    if (kSwiglu) t.rw = rs.weight(row0 + tid);
   }
   if (!kSwiglu) {
     t.b0 = g.b_scale[static_cast<int64_t>(e) * g.n + unit * 64 + rl];
@@ -170,44 +182,50 @@ __device__ __forceinline__ TileScales tile_scales(const GemmArgs& g, const RowSr
   return t;
 }
 
+__device__ __forceinline__ void publish_tile_scales(TileTables& tt, const TileScaleRegs& t, int mrows) {
+  const int tid = opaque_tid();
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  if (tid < mrows) {
+    tt.xs[tid] = t.xs;
+    tt.rw[tid] = t.rw;
+  }
+  tt.bs[wave][0][lane] = t.b0;
+  tt.bs[wave][1][lane] = t.b1;
+}
+
 // Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
-// the tile (mrows <= 64), 64-column unit `unit` of the output (SwiGLU: 32 channels). Row r's
-// scale and route weight reach the lanes that need them from lane r of `sc` by shuffles.
-template <bool kGather, bool kSwiglu, int MT>
-__device__ __forceinline__ void store_tile(const GemmArgs& g, const RowSrc& rs,
-                                           const v16f (&acc)[MT][2], int e, int row0, int mrows,
-                                           int unit, const TileScales& sc) {
-  const int lane = opaque_tid() & (kWave - 1);
+// the output (mrows <= 64; table row trow0 + r holds row r's scales), 64-column unit `unit`
+// of the output (SwiGLU: 32 channels).
+template <bool kSwiglu, int MT>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[MT][2], int row0,
+                                           int mrows, int unit, const TileTables& tt, int trow0) {
+  const int tid = opaque_tid();
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
   const int rl = lane & 31, hk = lane >> 5;
-  const float m_xs = sc.xs, m_rw = sc.rw;
-  if (!kSwiglu) {
-    const float bs[2] = {sc.b0, sc.b1};
+  const float b0 = tt.bs[wave][0][lane], b1 = tt.bs[wave][1][lane];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+  for (int mt = 0; mt < MT; ++mt) {
+    // the 16 rows' table entries read at once (rows past mrows read entries never used)
+    float xs[16], rw[16];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
-        const float xs = __shfl(m_xs, r, kWave);
-        if (r < mrows) {
-          uint16_t* crow = g.c + static_cast<int64_t>(row0 + r) * g.n + unit * 64 + rl;
+    for (int v = 0; v < 16; ++v) {
+      const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
+      xs[v] = tt.xs[trow0 + r];
+      rw[v] = kSwiglu ? tt.rw[trow0 + r] : 0.0f;
+    }
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) crow[ct * 32] = f32_to_bf16(acc[mt][ct][v] * xs * bs[ct]);
-        }
+    for (int v = 0; v < 16; ++v) {
+      const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
+      if (r >= mrows) continue;
+      if (!kSwiglu) {
+        uint16_t* crow = g.c + static_cast<int64_t>(row0 + r) * g.n + unit * 64 + rl;
+        crow[0] = f32_to_bf16(acc[mt][0][v] * xs[v] * b0);
+        crow[32] = f32_to_bf16(acc[mt][1][v] * xs[v] * b1);
+      } else {
+        g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl] =
+            swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs[v], b0, b1, rw[v]);
       }
-  } else {
-    const int chan = unit * 32 + rl;
-    const float wsg = sc.b0, wsu = sc.b1;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
-        const float xs = __shfl(m_xs, r, kWave);
-        const float rw = __shfl(m_rw, r, kWave);
-        if (r < mrows)
-          g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + chan] =
-              swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs, wsg, wsu, rw);
-      }
+    }
   }
 }
 
@@ -234,7 +252,7 @@ __device__ __forceinline__ int swizzle_piece(int p, int r) { return (p & ~7) | (
 // weight loads of chunk c and cost no wait at all by then.
 template <bool kGather, bool kSwiglu, int MT, bool kFast>
 __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
-                            uint8_t* smem) {
+                            uint8_t* smem, TileTables& tt) {
   constexpr int D = kFast ? kStreamDepth : 1;
   constexpr int kFullChunk = kAChunk / (32 * MT);  // k-bytes per chunk
   const int kc = kFast ? kFullChunk : 128;
@@ -318,6 +336,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
     }
   };
 
+  const TileScaleRegs tsr = load_tile_scales<kGather, kSwiglu>(g, rs, e, row0, mrows, unit);
   load_chunk(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -326,6 +345,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
     __builtin_amdgcn_sched_barrier(0);
   }
   store_chunk(0);
+  publish_tile_scales(tt, tsr, mrows);
   lds_barrier();
   for (int c = 0; c + 1 < nchunks; ++c) {
     load_chunk(c + 1);
@@ -341,7 +361,6 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
     store_chunk(c + 1);  // its buffer was last read in chunk c - 1, before the last barrier
     lds_barrier();
   }
-  const TileScales sc = tile_scales<kGather, kSwiglu>(g, rs, e, row0, mrows, unit);
   {
     const int c = nchunks - 1;
     for (int j = 0; j + D < spc; j += D) {
@@ -357,7 +376,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
   }
 
   if (!active) return;
-  store_tile<kGather, kSwiglu, MT>(g, rs, acc, e, row0, mrows, unit, sc);
+  store_tile<kSwiglu, MT>(g, acc, row0, mrows, unit, tt, 0);
 }
 
 // ------------------------------------------------------------------ TILE engine
@@ -371,7 +390,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
 // read 256 contiguous bytes of B, and 8 lanes read 8 distinct 16-byte bank groups of A.
 template <bool kGather, bool kSwiglu>
 __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
-                          uint8_t* smem) {
+                          uint8_t* smem, TileTables& tt) {
   constexpr int BK = kTileBK;
   constexpr int TM = kTileBM / kTileWM / 32, TN = kTileBN / kTileWN / 32;  // 4 x 2
   constexpr int kALoads = kTileBM * BK / 16 / kGemmThreads;  // 4
@@ -478,8 +497,12 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     }
   };
 
+  // a partial column block leaves waves without columns: their scales come from any valid unit
+  const TileScaleRegs tsr =
+      load_tile_scales<kGather, kSwiglu>(g, rs, e, row0, mrows, unit < units ? unit : units - 1);
   load_stage(0);
   store_stage(0);
+  publish_tile_scales(tt, tsr, mrows);
   __syncthreads();
   for (int kt = 0; kt < k_steps; ++kt) {
     const int cur = kt & 1;
@@ -492,11 +515,10 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   static_assert(TN == 2 && TM == 4, "a wave's tile is 128 rows x 64 columns");
   const int wrow = row0 + wm * (TM * 32);
   const int wrows = mrows - wm * (TM * 32);
-  store_tile<kGather, kSwiglu, 2>(g, rs, *reinterpret_cast<const v16f(*)[2][2]>(&acc[0]), e, wrow,
-                                  wrows, unit, tile_scales<kGather, kSwiglu>(g, rs, e, wrow, wrows, unit));
-  store_tile<kGather, kSwiglu, 2>(g, rs, *reinterpret_cast<const v16f(*)[2][2]>(&acc[2]), e, wrow + 64,
-                                  wrows - 64, unit,
-                                  tile_scales<kGather, kSwiglu>(g, rs, e, wrow + 64, wrows - 64, unit));
+  store_tile<kSwiglu, 2>(g, *reinterpret_cast<const v16f(*)[2][2]>(&acc[0]), wrow, wrows, unit, tt,
+                         wm * (TM * 32));
+  store_tile<kSwiglu, 2>(g, *reinterpret_cast<const v16f(*)[2][2]>(&acc[2]), wrow + 64, wrows - 64,
+                         unit, tt, wm * (TM * 32) + 64);
 }
 
 // ------------------------------------------------------------------ WIDE engine
@@ -513,16 +535,33 @@ __device__ void tile_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
 // group. Tiles are independent (prologue, stages, epilogue): a software pipeline across the
 // tiles of a workgroup needed the next tile's offsets live through the stage loop and the
 // compiler spilled (measured slower).
+//
+// Two shapes (BM = rows of a full tile): BM = 256 with one workgroup per CU (512 registers a
+// lane), and BM = 128 with two workgroups per CU (256 registers a lane, 128 AGPR accumulators):
+// then each SIMD runs two waves of different tiles, and one tile's prologue and epilogue overlap
+// the other's MFMAs. The B ring and the A operand look-ahead are shallower at BM = 128 (the
+// other wave covers the latency).
 constexpr int kWideThreads = 256, kWideWaves = 4;
 constexpr int kWideBK = 128;
-constexpr int kWideStage = kTileBM * kWideBK;  // 32 KB of A
 constexpr int kWideBufs = 3;
-// after the A ring: the tile's scale table (its 256 row scales, then its 256 weight-row scales)
-constexpr int kWideTables = kWideBufs * kWideStage;
-// the tables: 256 row scales, 256 weight-row scales (f32), then (GEMM2) 256 row addresses (u64)
-constexpr int kWideSmemBytes = kWideTables + 2 * kTileBM * 4 + kTileBM * 8;
-constexpr int kWideRing = 4;  // 64-k steps of B in registers
 constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that select it
+
+template <int BM>
+struct WideShape {
+  static_assert(BM == 256 || BM == 128, "full tile of 256 or 128 rows");
+  static constexpr int kStage = BM * kWideBK;  // bytes of one A stage
+  // after the A ring, the tile's tables: BM row scales, the 256 weight-row scales (f32), then
+  // (GEMM2) BM row addresses (u64)
+  static constexpr int kTables = kWideBufs * kStage;
+  static constexpr int kColScales = BM * 4;
+  static constexpr int kAddrs = kColScales + kWideWaves * kStreamUnit * 4;
+  static constexpr int kSmemBytes = kTables + kAddrs + BM * 8;
+  static constexpr int kRing = BM == 256 ? 4 : 2;  // 64-k steps of B in registers
+  static constexpr int kWavesPerSimd = BM == 256 ? 1 : 2;
+  static constexpr int kFullTM = BM / 32;
+  // the epilogue stages each wave's 64 output rows (8 KB) in the A ring's first bytes
+  static_assert(kWideWaves * 8192 <= kTables, "epilogue staging fits the A ring");
+};
 
 // Epilogue of a WIDE tile. The MFMAs run transposed (weights as the first operand), so lane
 // l holds token row tm*32 + l%32 and, per 32-column tile tn, the columns 8*(v/4) + 4*(l/32) +
@@ -536,16 +575,17 @@ constexpr int kWideMinRowsPerExpert = kTileBM;  // average routed rows that sele
 // gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
 // bf16 partials (-0 as +0) to the row addresses of the tile's table: its part row, or for a
 // row whose token has no other routed slot its y row (row_dest).
-template <bool kGather, bool kGemm1, int TM>
+template <bool kGather, bool kGemm1, int BM, int TM>
 __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[TM][2], int row0,
                                            int mrows, int unit, uint8_t* stage,
                                            const uint8_t* table) {
+  using W = WideShape<BM>;
   const int tid = opaque_tid();
   const int lane = tid & (kWave - 1);
   const int rl = lane & 31, hk = lane >> 5;
   const float* s_xs = reinterpret_cast<const float*>(table);
-  const float* s_bs = s_xs + kTileBM + (tid / kWave) * kStreamUnit;
-  const uint64_t* s_addr = reinterpret_cast<const uint64_t*>(table + 2 * kTileBM * 4);  // GEMM2
+  const float* s_bs = reinterpret_cast<const float*>(table + W::kColScales) + (tid / kWave) * kStreamUnit;
+  const uint64_t* s_addr = reinterpret_cast<const uint64_t*>(table + W::kAddrs);  // GEMM2
   float4 bs[2][4];
 #pragma unroll
   for (int tn = 0; tn < 2; ++tn)
@@ -606,11 +646,16 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
   }
 }
 
-// TM row tiles of 32: 8 for a full tile; 4, 2 or 1 for an expert's last tile of at most 128,
-// 64 or 32 rows (a fraction of the MFMAs and A traffic for the row remainder).
-template <bool kGather, bool kSwiglu, int TM>
+// TM row tiles of 32: BM/32 for a full tile; fewer (4, 2 or 1) for an expert's last tile of
+// at most 128, 64 or 32 rows (a fraction of the MFMAs and A traffic for the row remainder).
+template <bool kGather, bool kSwiglu, int BM, int TM>
 __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
                           uint8_t* smem) {
+  using W = WideShape<BM>;
+  constexpr int kWideStage = W::kStage;
+  constexpr int kWideTables = W::kTables;
+  constexpr int kWideRing = W::kRing;
+  static_assert(TM <= W::kFullTM, "a tile of at most BM rows");
   constexpr int TN = kStreamUnit / 32;                        // 2
   constexpr int kALoads = TM * 32 * kWideBK / 16 / kWideThreads;  // TM
   constexpr int kRowsPerLoad = kWideThreads / (kWideBK / 16);     // 32
@@ -679,7 +724,8 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   // stage's first operands, whose buffer is complete since the previous barrier), which
   // covers the LDS latency with one wave per SIMD. Order pinned by sched_barrier.
   constexpr int kGroups = (kWideBK / 64) * TM;
-  constexpr int kAhead = kGroups >= 4 ? 3 : kGroups - 1;  // TM = 1: two groups a stage
+  // one wave a SIMD: read 3 groups ahead; two (BM = 128): 1; TM = 1 has two groups a stage
+  constexpr int kAhead = W::kWavesPerSimd == 1 ? (kGroups >= 4 ? 3 : kGroups - 1) : 1;
   static_assert(kGroups % (kAhead + 1) == 0, "operand ring index must repeat per stage");
   v8i abuf[kAhead + 1];
   auto read_group = [&](int kt, int gi) {
@@ -744,11 +790,11 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     *reinterpret_cast<int4*>(smem + a_dst0 + i * kRowsPerLoad * kWideBK) = ra0[i];  // stage 0, buffer 0
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) store_a(1, i, 1);
-  reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
-  reinterpret_cast<float*>(smem + kWideTables)[kTileBM + tid] = pre_bs;
-  if (!kSwiglu) {
+  if (tid < BM) reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
+  reinterpret_cast<float*>(smem + kWideTables + W::kColScales)[tid] = pre_bs;
+  if (!kSwiglu && tid < BM) {
     const int prow = row0 + min(tid, mrows - 1);
-    reinterpret_cast<uint64_t*>(smem + kWideTables + 2 * kTileBM * 4)[tid] =
+    reinterpret_cast<uint64_t*>(smem + kWideTables + W::kAddrs)[tid] =
         pre_on != 0 && pre_dest >= 0 ? reinterpret_cast<uint64_t>(g.y_direct + static_cast<int64_t>(pre_dest) * g.n)
                                      : reinterpret_cast<uint64_t>(g.c + static_cast<int64_t>(prow) * g.n);
   }
@@ -760,11 +806,11 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   // compiler's load counting exact
   for (int kt = 0; kt < stages; kt += 2) {  // stages is even (k % 256 == 0)
     stage(kt, 0, 0, 1);
-    stage(kt + 1, 2, 1, 0);
+    stage(kt + 1, kWideRing == 4 ? 2 : 0, 1, 0);  // a ring of 2 refills the same two slots
   }
   // every wave has passed its last LDS read of A (the barrier that ended the last stage)
   if (!active) return;
-  store_wide<kGather, kSwiglu, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
+  store_wide<kGather, kSwiglu, BM, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
 }
 
 // ------------------------------------------------------------------ in-kernel routing
@@ -870,7 +916,7 @@ __device__ __forceinline__ int stream_blocks(const GemmArgs& g) {
 // A STREAM item is one (64-row chunk, 512-column block); a TILE item is one 256 x 256 tile
 // (row-block major).
 __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const int* s_count,
-                           bool all_tile = false) {
+                           bool all_tile = false, int tile_rows = kTileBM) {
   const int E = g.num_experts;
   const int lane = lane_id();
   const int stream_nb = stream_blocks(g);
@@ -884,7 +930,7 @@ __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const 
         const int cnt = s_count[e];
         const bool tile = all_tile || g.engine == GemmEngine::kTile ||
                           (g.engine == GemmEngine::kAuto && cnt > kStreamRows);
-        items = tile ? (cnt + kTileBM - 1) / kTileBM * tile_nb
+        items = tile ? (cnt + tile_rows - 1) / tile_rows * tile_nb
                      : (cnt + kStreamRows - 1) / kStreamRows * stream_nb;
         s_tile[e] = tile;
       }
@@ -940,8 +986,9 @@ __device__ __forceinline__ ItemDeal deal_items(int total) {
 // TILE item `local` of an expert with cnt rows -> (row block mt, column block nb): row blocks
 // in groups of 4, columns inside a group, so that the consecutive items an XCD runs together
 // form 4 x 8 tiles sharing A rows and B columns in its L2.
-__device__ __forceinline__ void tile_coords(int local, int cnt, int tile_nb, int& mt, int& nb) {
-  const int mblocks = (cnt + kTileBM - 1) / kTileBM;
+__device__ __forceinline__ void tile_coords(int local, int cnt, int tile_nb, int& mt, int& nb,
+                                            int tile_rows = kTileBM) {
+  const int mblocks = (cnt + tile_rows - 1) / tile_rows;
   const int group = local / (4 * tile_nb);
   const int in_group = local - group * 4 * tile_nb;
   const int rows_in_group = min(4, mblocks - group * 4);
@@ -964,6 +1011,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   __shared__ float s_rw[kRowTable];
   __shared__ int s_task[kRowTable];
   __shared__ uint8_t s_ev[kFusedMaxTasks];  // in-kernel routing: expert of each task
+  __shared__ TileTables s_tt;                // the current item's scales (epilogue)
   const int E = g.num_experts;
   const bool fused = kSwiglu && g.route_in_kernel;
   const RouteArgs& ra = g.route;
@@ -1052,7 +1100,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
         rs = RowSrc{s_tok, s_rw, off_e + r0};
       }
       tile_tile<kGather, kSwiglu>(g, rs, e, off_e + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM),
-                                  nb, smem);
+                                  nb, smem, s_tt);
     } else {
       const int mc = local / stream_nb;
       const int nb = local - mc * stream_nb;
@@ -1066,21 +1114,21 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
         rs = RowSrc{s_tok, s_rw, row0};
       }
       if (mrows > 32) {
-        if (fast2) stream_tile<kGather, kSwiglu, 2, true>(g, rs, e, row0, mrows, nb, smem);
-        else if (kAnyK) stream_tile<kGather, kSwiglu, 2, false>(g, rs, e, row0, mrows, nb, smem);
+        if (fast2) stream_tile<kGather, kSwiglu, 2, true>(g, rs, e, row0, mrows, nb, smem, s_tt);
+        else if (kAnyK) stream_tile<kGather, kSwiglu, 2, false>(g, rs, e, row0, mrows, nb, smem, s_tt);
       } else {
-        if (fast1) stream_tile<kGather, kSwiglu, 1, true>(g, rs, e, row0, mrows, nb, smem);
-        else if (kAnyK) stream_tile<kGather, kSwiglu, 1, false>(g, rs, e, row0, mrows, nb, smem);
+        if (fast1) stream_tile<kGather, kSwiglu, 1, true>(g, rs, e, row0, mrows, nb, smem, s_tt);
+        else if (kAnyK) stream_tile<kGather, kSwiglu, 1, false>(g, rs, e, row0, mrows, nb, smem, s_tt);
       }
     }
     __syncthreads();
   }
 }
 
-// Persistent dispatcher of the WIDE engine: every expert's rows as 256 x 256 tiles, items dealt
+// Persistent dispatcher of the WIDE engine: every expert's rows as BM x 256 tiles, items dealt
 // to the XCDs in contiguous ranges like the 8-wave dispatcher's.
-template <bool kGather, bool kSwiglu>
-__global__ __launch_bounds__(kWideThreads, 1) void wide_gemm_kernel(GemmArgs g) {
+template <bool kGather, bool kSwiglu, int BM>
+__global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wide_gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_prefix[kMaxGemmExperts + 1];
   __shared__ int s_tile[kMaxGemmExperts];
@@ -1092,7 +1140,7 @@ __global__ __launch_bounds__(kWideThreads, 1) void wide_gemm_kernel(GemmArgs g) 
     s_off[e] = g.offsets[e];
   }
   __syncthreads();
-  plan_items(g, s_prefix, s_tile, s_count, true);
+  plan_items(g, s_prefix, s_tile, s_count, true, BM);
   __syncthreads();
   const int total = s_prefix[E];
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
@@ -1104,17 +1152,17 @@ __global__ __launch_bounds__(kWideThreads, 1) void wide_gemm_kernel(GemmArgs g) 
     const int e = expert_of_item(s_prefix, E, t);
     const int cnt = s_count[e];
     int mt, nb;
-    tile_coords(t - s_prefix[e], cnt, tile_nb, mt, nb);
-    const int mrows = min(kTileBM, cnt - mt * kTileBM);
-    const int row0 = s_off[e] + mt * kTileBM;
-    if (mrows > 128)
-      wide_tile<kGather, kSwiglu, 8>(g, rs, e, row0, mrows, nb, smem);
+    tile_coords(t - s_prefix[e], cnt, tile_nb, mt, nb, BM);
+    const int mrows = min(BM, cnt - mt * BM);
+    const int row0 = s_off[e] + mt * BM;
+    if (BM == 256 && mrows > 128)
+      wide_tile<kGather, kSwiglu, BM, (BM == 256 ? 8 : 4)>(g, rs, e, row0, mrows, nb, smem);
     else if (mrows > 64)
-      wide_tile<kGather, kSwiglu, 4>(g, rs, e, row0, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, BM, 4>(g, rs, e, row0, mrows, nb, smem);
     else if (mrows > 32)
-      wide_tile<kGather, kSwiglu, 2>(g, rs, e, row0, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, BM, 2>(g, rs, e, row0, mrows, nb, smem);
     else
-      wide_tile<kGather, kSwiglu, 1>(g, rs, e, row0, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, BM, 1>(g, rs, e, row0, mrows, nb, smem);
     __syncthreads();
   }
 }
@@ -1134,18 +1182,19 @@ hipError_t ensure_dynamic_lds(int bytes) {
   return err;
 }
 
-template <bool kGather, bool kSwiglu>
+template <bool kGather, bool kSwiglu, int BM>
 hipError_t launch_wide(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
-  {  // the 104 KB of dynamic LDS exceeds the default limit
-    const hipError_t err = ensure_dynamic_lds<&wide_gemm_kernel<kGather, kSwiglu>>(kWideSmemBytes);
+  using W = WideShape<BM>;
+  {  // the dynamic LDS (up to 104 KB) exceeds the default limit
+    const hipError_t err = ensure_dynamic_lds<&wide_gemm_kernel<kGather, kSwiglu, BM>>(W::kSmemBytes);
     if (err != hipSuccess) return err;
   }
   const int64_t bound =
-      (static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * ((g.n + kTileBN - 1) / kTileBN);
-  int64_t grid = num_cus;  // one 4-wave workgroup per CU
+      (static_cast<int64_t>(max_rows) / BM + g.num_experts) * ((g.n + kTileBN - 1) / kTileBN);
+  int64_t grid = static_cast<int64_t>(num_cus) * W::kWavesPerSimd;  // workgroups a CU: 1 or 2
   if (grid > bound) grid = bound;
-  hipLaunchKernelGGL((wide_gemm_kernel<kGather, kSwiglu>), dim3(static_cast<unsigned>(grid)),
-                     dim3(kWideThreads), kWideSmemBytes, stream, g);
+  hipLaunchKernelGGL((wide_gemm_kernel<kGather, kSwiglu, BM>), dim3(static_cast<unsigned>(grid)),
+                     dim3(kWideThreads), W::kSmemBytes, stream, g);
   return hipGetLastError();
 }
 
@@ -1194,6 +1243,13 @@ bool gemm_shape_supported(int n, int k) {
   return n > 0 && k > 0 && n % 128 == 0 && k % 128 == 0;
 }
 
+// Full WIDE tile heights. 256 rows (one workgroup a CU) for both GEMMs: with 128-row tiles and
+// two workgroups a CU, GEMM1 (weights read twice as often) ran 1.33x slower at the 196K-row
+// prefill; GEMM2 ran 7% faster at 24.7K rows but slower at 196K rows, where it also left the
+// next layer's GEMM1 2% slower (measured on one box, builds alternated).
+constexpr int kWideBM1 = 256;
+constexpr int kWideBM2 = 256;
+
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
   if (max_rows <= 0) return hipSuccess;
   if (g.num_experts > kMaxGemmExperts) return hipErrorInvalidValue;
@@ -1204,11 +1260,11 @@ hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hip
     return hipErrorInvalidValue;
   if (g.sw.enabled) {
     if (g.row_token == nullptr || g.n != 2 * g.sw.inter) return hipErrorInvalidValue;
-    return wide ? launch_wide<true, true>(g, max_rows, num_cus, stream)
+    return wide ? launch_wide<true, true, kWideBM1>(g, max_rows, num_cus, stream)
                 : launch_engines<true, true>(g, max_rows, num_cus, stream);
   }
   if (g.row_token != nullptr) return hipErrorInvalidValue;
-  return wide ? launch_wide<false, false>(g, max_rows, num_cus, stream)
+  return wide ? launch_wide<false, false, kWideBM2>(g, max_rows, num_cus, stream)
               : launch_engines<false, false>(g, max_rows, num_cus, stream);
 }
 
