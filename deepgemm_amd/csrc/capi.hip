@@ -59,6 +59,7 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->act_offset = take(rows * static_cast<int64_t>(intermediate));
   l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
   l->row_dest_offset = take(rows * 4);
+  l->sched_offset = take(2 * mmoe::kSchedInts * 4);
   l->total_bytes = off;
 }
 
@@ -158,6 +159,8 @@ mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratc
   r.row_token = at<int32_t>(ws, l.row_token_offset);
   r.row_weight = at<float>(ws, l.row_weight_offset);
   r.m_indices = at<int32_t>(ws, l.m_indices_offset);
+  r.zero_ints = at<int32_t>(ws, l.sched_offset);  // the GEMMs' claim counters start at zero
+  r.zero_count = 2 * mmoe::kSchedInts;
   return r;
 }
 
@@ -338,6 +341,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   g1.sw.y = at<float>(ws, l.y_offset);
   g1.sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
   g1.sw.clamp = a->activation_clamp;
+  g1.sched = at<int32_t>(ws, l.sched_offset);
   if (route_in_gemm1) {
     g1.route_in_kernel = 1;
     g1.route = forward_route_args(a, l);
@@ -357,6 +361,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   g2.c = at<uint16_t>(ws, l.part_offset);
   g2.n = a->hidden;
   g2.k = a->intermediate;
+  g2.sched = at<int32_t>(ws, l.sched_offset) + mmoe::kSchedInts;
   // Prefill: rows whose token has a single routed slot leave the WIDE GEMM2 straight into y
   // (the combine's one-term sum), so the combine neither reads nor writes them. The requant
   // builds the row table and sets meta[2]; GEMM2 and the combine follow meta[2] on the device,

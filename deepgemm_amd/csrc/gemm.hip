@@ -983,6 +983,41 @@ __device__ __forceinline__ ItemDeal deal_items(int total) {
                   static_cast<int>(static_cast<int64_t>(total) * (xcd + 1) / 8), nwg / 8, b / 8};
 }
 
+// Dynamic dealing (WIDE kernel). The same XCD ranges, but only each workgroup's first item is
+// fixed (position `slot` of its range); after that it claims the next item of its range from
+// the range's counter (one device atomic a tile, issued when the tile starts and read when it
+// ends, so its latency hides behind the tile), and when its range runs out, from the other
+// XCDs' ranges in turn. Claims follow item order, so the tiles an XCD runs together stay
+// neighbours (shared L2 traffic), while fast workgroups take more items than slow ones: tiles of
+// unequal cost (an expert's short last row block) and a range that does not divide evenly no
+// longer leave some workgroups with a whole extra tile. Every claim only moves a counter
+// forward, so the loop ends; the last workgroup to finish resets the counters to zero.
+struct Claims {
+  int32_t* sched;  // [0..7] claim counters, [8] finished workgroups
+  int total, nranges, home, step, slot;
+  __device__ __forceinline__ int begin(int r) const { return static_cast<int>(static_cast<int64_t>(total) * r / nranges); }
+  __device__ __forceinline__ int end(int r) const { return static_cast<int>(static_cast<int64_t>(total) * (r + 1) / nranges); }
+  __device__ __forceinline__ int range(int ri) const { return (home + ri) % nranges; }
+  // claimed index c of range r -> the item (the first `step` items are the fixed first items)
+  __device__ __forceinline__ int item(int r, int c) const { return begin(r) + step + c; }
+  // thread 0: the next item from range index ri on (advancing ri past exhausted ranges), or -1
+  __device__ int claim_from(int& ri) const {
+    for (; ri < nranges; ++ri) {
+      const int r = range(ri);
+      const int t = item(r, atomicAdd(&sched[r], 1));
+      if (t < end(r)) return t;
+    }
+    return -1;
+  }
+};
+
+__device__ __forceinline__ Claims make_claims(int32_t* sched, int total) {
+  const int nwg = static_cast<int>(gridDim.x);
+  const int b = static_cast<int>(blockIdx.x);
+  const int nranges = nwg % 8 == 0 ? 8 : 1;
+  return Claims{sched, total, nranges, nranges == 8 ? b % 8 : 0, nwg / nranges, nranges == 8 ? b / 8 : b};
+}
+
 // TILE item `local` of an expert with cnt rows -> (row block mt, column block nb): row blocks
 // in groups of 4, columns inside a group, so that the consecutive items an XCD runs together
 // form 4 x 8 tiles sharing A rows and B columns in its L2.
@@ -1144,11 +1179,8 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
   __syncthreads();
   const int total = s_prefix[E];
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
-  const ItemDeal deal = deal_items(total);
   const RowSrc rs{g.row_token, g.sw.row_weight, 0};
-  for (int k = 0; k < deal.rounds(); ++k) {
-    const int t = deal.item(k);
-    if (t >= deal.end) continue;  // the last round's short tail (uniform in the workgroup)
+  auto run_item = [&](int t) {
     const int e = expert_of_item(s_prefix, E, t);
     const int cnt = s_count[e];
     int mt, nb;
@@ -1163,7 +1195,59 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
       wide_tile<kGather, kSwiglu, BM, 2>(g, rs, e, row0, mrows, nb, smem);
     else
       wide_tile<kGather, kSwiglu, BM, 1>(g, rs, e, row0, mrows, nb, smem);
+  };
+  // One item at a time from the static deal or from the claims. Claiming only pays when a
+  // workgroup has few items (the last round's granularity is then a large share of its work;
+  // 24.7K routed rows: 7 items a workgroup, 5% faster); with many it measured slower (196K rows,
+  // 49 items: 1% slower; 49K Zipf rows, 13 items: 1% slower) -- the lockstep rounds of the static
+  // deal keep an XCD's concurrent tiles on the same rows and weights, and at those sizes the
+  // chip is power-bound, so idle workgroups cost less than the looser L2 sharing.
+  constexpr int kClaimMaxItemsPerWg = 10;
+  const bool dynamic =
+      g.sched != nullptr && total <= kClaimMaxItemsPerWg * static_cast<int>(gridDim.x);
+  const ItemDeal deal = deal_items(total);
+  const Claims cl = make_claims(g.sched, total);
+  __shared__ int s_item;
+  int k = 0;   // static: the round
+  int ri = 0;  // dynamic, thread 0: index of the range it claims from
+  if (threadIdx.x == 0 && dynamic) {
+    const int first = cl.begin(cl.home) + cl.slot;
+    s_item = first < cl.end(cl.home) ? first : cl.claim_from(ri);
+  }
+  __syncthreads();
+  while (true) {
+    int t;
+    if (dynamic) {
+      t = s_item;
+    } else {
+      for (t = -1; k < deal.rounds() && t < 0; ++k) {
+        const int c = deal.item(k);
+        t = c < deal.end ? c : -1;  // the last round's short tail
+      }
+    }
+    if (t < 0) break;
+    int pending = 0;  // thread 0: the claim for the item after this one, issued now
+    if (dynamic && threadIdx.x == 0 && ri < cl.nranges) pending = atomicAdd(&g.sched[cl.range(ri)], 1);
+    run_item(t);
+    if (dynamic && threadIdx.x == 0) {
+      int next = -1;
+      if (ri < cl.nranges) {
+        const int r = cl.range(ri);
+        next = cl.item(r, pending);
+        if (next >= cl.end(r)) {
+          ++ri;
+          next = cl.claim_from(ri);
+        }
+      }
+      s_item = next;  // read after the barrier; rewritten only after the next tile's barriers
+    }
     __syncthreads();
+  }
+  if (dynamic && threadIdx.x == 0) {  // every claim of this workgroup is done: count it out
+    if (atomicAdd(&g.sched[8], 1) == static_cast<int>(gridDim.x) - 1) {
+      for (int r = 0; r < 8; ++r) atomicExch(&g.sched[r], 0);
+      atomicExch(&g.sched[8], 0);
+    }
   }
 }
 

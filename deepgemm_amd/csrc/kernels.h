@@ -29,6 +29,8 @@ struct RouteArgs {
   int32_t* row_token;             // [rows]
   float* row_weight;              // [rows] or null
   int32_t* m_indices;             // [rows] or null
+  int32_t* zero_ints;             // zeroed by the routing launch (the GEMMs' claim counters), or null
+  int zero_count;
 };
 
 // Count -> offsets -> stable scatter over at most max_tasks = S*K tasks. Deterministic: rows
@@ -73,7 +75,11 @@ struct GemmArgs {
   const int32_t* row_dest;
   uint16_t* y_direct;
   const int32_t* direct_flag;
+  // WIDE kernel work claiming (kSchedInts ints, zero at launch; the kernel leaves them zero):
+  // [0..7] per-XCD claim counters, [8] finished workgroups. Null: static dealing.
+  int32_t* sched;
 };
+constexpr int kSchedInts = 16;
 
 // Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
 // a_scale[r] * b_scale[e,n]). Persistent: the grid strides over the tiles, enumerated on the

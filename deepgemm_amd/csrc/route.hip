@@ -102,7 +102,14 @@ __device__ void publish_offsets(const RouteArgs& a, const int* s_tot, int* s_off
   }
 }
 
+// The routing launch runs before the GEMMs of a layer: it zeroes their claim counters.
+__device__ __forceinline__ void zero_sched(const RouteArgs& a) {
+  if (blockIdx.x == 0 && a.zero_ints != nullptr)
+    for (int i = threadIdx.x; i < a.zero_count; i += blockDim.x) a.zero_ints[i] = 0;
+}
+
 __global__ __launch_bounds__(kSmallThreads) void route_small_kernel(RouteArgs a) {
+  zero_sched(a);
   __shared__ int s_cnt[kSmallWaves][kSmallMaxExperts];
   __shared__ int s_tot[kSmallMaxExperts];
   __shared__ int s_off[kSmallMaxExperts + 1];
@@ -135,6 +142,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_small_kernel(RouteArgs a)
 
 __global__ __launch_bounds__(kChunkThreads) void route_count_kernel(RouteArgs a, int chunk_tasks) {
   __shared__ int s_cnt[kMaxExperts];
+  zero_sched(a);
   const int tid = threadIdx.x;
   for (int e = tid; e < a.num_experts; e += kChunkThreads) s_cnt[e] = 0;
   __syncthreads();

@@ -236,7 +236,9 @@ class SymmBuffer:
                                                   ctypes.byref(self.scratch_layout)),
                     "SymmBuffer")
         self.buffer = torch.zeros((layout.total_bytes,), dtype=torch.int8, device="cuda")
-        self.route_scratch = torch.empty((nbytes.value,), dtype=torch.int8, device="cuda")
+        # zeroed once: the prefill GEMMs' work-claim counters live here (a full call's routing
+        # stage zeroes them too, and the GEMMs leave them at zero)
+        self.route_scratch = torch.zeros((nbytes.value,), dtype=torch.int8, device="cuda")
         t = num_max_tokens_per_rank
 
         def view(off, count, dtype, shape):
@@ -299,6 +301,7 @@ class SymmBuffer:
             "act": (l.act_offset, torch.float8_e4m3fn, (rows, self.intermediate_hidden)),
             "part": (l.part_offset, torch.bfloat16, (rows, self.hidden)),
             "row_dest": (l.row_dest_offset, torch.int32, (rows,)),
+            "sched": (l.sched_offset, torch.int32, (2, 16)),
         }
         off, dtype, shape = spec[name]
         n = 1

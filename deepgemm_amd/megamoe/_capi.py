@@ -54,6 +54,7 @@ class ScratchLayout(ctypes.Structure):
         ("act_offset", c_i64),
         ("part_offset", c_i64),
         ("row_dest_offset", c_i64),
+        ("sched_offset", c_i64),
     ]
 
 

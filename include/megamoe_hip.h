@@ -96,6 +96,9 @@ typedef struct mmoe_scratch_layout {
                                   single routed slot go straight to y instead (row_dest) */
   int64_t row_dest_offset;     /* int32 [rows] token of a row written straight to y, else -1
                                   (valid after a call that used it) */
+  int64_t sched_offset;        /* int32 [2, 16] work-claim counters of the prefill GEMM kernels
+                                  (GEMM1, GEMM2): zeroed by the routing stage, left at zero by
+                                  the GEMMs themselves */
 } mmoe_scratch_layout;
 
 #define MMOE_ROUTE_CHUNK 1024
