@@ -887,7 +887,7 @@ __device__ void fused_rows(const RouteArgs& a, int ntasks, int e, int cnt, int o
   }
   __syncthreads();
   const int n = min(kRowTable, cnt - r_lo);
-  for (int t = static_cast<int>(threadIdx.x); t < n; t += kGemmThreads) {
+  for (int t = opaque_tid(); t < n; t += kGemmThreads) {  // recomputed, not kept live across items
     const int task = s_task[t];
     const float w = s_task_w != nullptr ? s_task_w[task] : a.topk_w[task];
     s_rw[t] = w;
