@@ -488,6 +488,27 @@ def test_layer_prefill_full_scale_sampled(mm, cuda, full_weights, cfg):
     assert torch.equal(y1, y), "two calls bitwise identical"
 
 
+def test_wide_claim_counters_return_to_zero(mm, cuda):
+    """The WIDE GEMMs claim items from per-XCD counters in route_scratch when a workgroup has few
+    items; the last workgroup of each GEMM resets them, so after a call (and after a GEMM2 run on
+    its own) they read zero again, and a second call on the same scratch is bitwise identical."""
+    s, e, hdim, inter, k = 2048, 4, 512, 256, 6
+    x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=31, global_experts=8)
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=32, mm=mm)
+    buf = mm.SymmBuffer(None, e, s, k, hdim, inter)
+    log("WIDE claim counters")
+    y1 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2).clone()
+    torch.cuda.synchronize()
+    assert buf.scratch_view("meta")[1].item() == 1, "the WIDE GEMM1 ran"
+    assert torch.all(buf.scratch_view("sched").cpu() == 0)
+    mm.LayerCall(torch.empty_like(y1), l1, l2, buf).run(3, 3)  # GEMM2 alone
+    torch.cuda.synchronize()
+    assert torch.all(buf.scratch_view("sched").cpu() == 0)
+    y2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
 def test_layer_no_routed_rows(mm, cuda):
     """Every slot invalid -> y == 0 exactly (no partial contributes)."""
     s, e, hdim, inter = 10, 4, 256, 128

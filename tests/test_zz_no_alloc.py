@@ -57,6 +57,28 @@ def test_static_scratch_matches_mmoe_forward(mm, cuda):
         assert int(stats_ref.sum()) > 0
 
 
+def test_static_scratch_wide_path(mm, cuda):
+    """A small shape with many rows per expert runs the prefill (WIDE) kernels, whose work-claim
+    counters then live in the static scratch too; twice in a row, bitwise equal to
+    mmoe_forward."""
+    e, hdim, inter, k = 4, 512, 256, 6
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=4322, mm=mm)
+    for s in (2048, 1536):
+        log(f"static scratch, WIDE path: S={s}")
+        x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=99 + s, global_experts=8)
+        buf = mm.get_symm_buffer_for_mega_moe(None, e, s, k, hdim, inter)
+        _load(buf, x_fp8, x_sf, idx, w)
+        y_ref = torch.empty((s, hdim), dtype=torch.bfloat16, device=cuda)
+        mm.fp8_w8a8_mega_moe(y_ref, l1, l2, buf)
+        torch.cuda.synchronize()
+        assert buf.scratch_view("meta")[1].item() == 1, "the WIDE GEMM1 ran"
+        y_got = torch.full((s, hdim), 7.0, dtype=torch.bfloat16, device=cuda)
+        st = _static_call(mm, y_got, l1, l2, buf)
+        assert st == 0, mm._capi.status_string(st)
+        torch.cuda.synchronize()
+        assert torch.equal(y_got.view(torch.int16), y_ref.view(torch.int16)), f"S={s}"
+
+
 def test_static_scratch_limit_is_refused(mm, cuda):
     """A capacity whose scratch exceeds MMOE_STATIC_SCRATCH_BYTES returns
     MMOE_ERR_STATIC_SCRATCH before any launch."""
