@@ -315,9 +315,21 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   const bool route_in_gemm1 = runs(MMOE_STAGE_ROUTE) && runs(MMOE_STAGE_GEMM1) &&
                               max_rows <= mmoe::gemm_route_max_tasks() &&
                               a->num_experts <= mmoe::gemm_route_max_experts();
+  // Graph replays (tokens read on the device) with a bound that selects the WIDE kernels: the
+  // routed rows choose between those and the 8-wave kernels on the device, so a replay with
+  // few live tokens in a large bucket still runs the decode engines; and when GEMM1 and the
+  // routing run together, the 8-wave GEMM1 also routes the live tasks itself when they fit
+  // (the routing launch then returns at once).
+  const int32_t* rows_on_device =
+      a->runtime_num_tokens != nullptr ? at<int32_t>(ws, l.meta_offset) : nullptr;
+  const bool route_small_in_gemm1 = rows_on_device != nullptr && !route_in_gemm1 &&
+                                    runs(MMOE_STAGE_ROUTE) && runs(MMOE_STAGE_GEMM1) &&
+                                    a->num_experts <= mmoe::gemm_route_max_experts();
   if (runs(MMOE_STAGE_ROUTE) && !route_in_gemm1) {
-    st = run_route(a, l, s);
-    if (st != MMOE_OK) return st;
+    mmoe::RouteArgs r = forward_route_args(a, l);
+    const int64_t tasks = static_cast<int64_t>(a->num_tokens) * a->num_topk;
+    if (route_small_in_gemm1) r.fused_max_tasks = mmoe::gemm_route_max_tasks();
+    if (mmoe::launch_route(r, tasks, s) != hipSuccess) return MMOE_ERR_HIP;
   }
 
   mmoe::GemmArgs g1;
@@ -346,7 +358,9 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     g1.route_in_kernel = 1;
     g1.route = forward_route_args(a, l);
   }
-  if (runs(MMOE_STAGE_GEMM1) && mmoe::launch_grouped_gemm(g1, max_rows, cus, s) != hipSuccess)
+  if (route_small_in_gemm1) g1.route = forward_route_args(a, l);
+  if (runs(MMOE_STAGE_GEMM1) &&
+      mmoe::launch_grouped_gemm(g1, max_rows, cus, s, rows_on_device, route_small_in_gemm1) != hipSuccess)
     return MMOE_ERR_HIP;
 
   mmoe::GemmArgs g2 = g1;
@@ -381,15 +395,20 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     g2.direct_flag = direct_flag;
   }
 
-  // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU
+  // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU (after a
+  // dual GEMM1 launch it finds out on the device which GEMM1 ran)
+  const bool wide1 = mmoe::gemm_wide_selected(g1, max_rows);
+  const bool dual1 = wide1 && rows_on_device != nullptr;
   if (runs(MMOE_STAGE_REQUANT) &&
-      mmoe::launch_requant(at<float>(ws, l.y_offset), mmoe::gemm_wide_selected(g1, max_rows), g1.sw,
-                           at<float>(ws, l.amax_offset), at<int32_t>(ws, l.meta_offset),
-                           at<uint8_t>(ws, l.act_offset), at<float>(ws, l.act_scale_offset),
-                           max_rows, a->intermediate, dest, cus, s) != hipSuccess)
+      mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, g1.sw, at<float>(ws, l.amax_offset),
+                           at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
+                           at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, dest,
+                           cus, s, dual1 ? rows_on_device : nullptr,
+                           mmoe::gemm_wide_min_rows(a->num_experts)) != hipSuccess)
     return MMOE_ERR_HIP;
 
-  if (runs(MMOE_STAGE_GEMM2) && mmoe::launch_grouped_gemm(g2, max_rows, cus, s) != hipSuccess)
+  if (runs(MMOE_STAGE_GEMM2) &&
+      mmoe::launch_grouped_gemm(g2, max_rows, cus, s, rows_on_device) != hipSuccess)
     return MMOE_ERR_HIP;
 
   if (runs(MMOE_STAGE_COMBINE)) {

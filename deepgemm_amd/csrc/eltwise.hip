@@ -36,6 +36,8 @@ struct RequantArgs {
   float* act_scale;
   int inter;
   RowDest dest;
+  const int32_t* dual_rows;  // dual launches: from h iff *dual_rows >= dual_min_rows
+  int dual_min_rows;
 };
 
 // channels 4q .. 4q+3 of row `row`
@@ -54,18 +56,18 @@ __device__ __forceinline__ float4 requant_load(const RequantArgs& r, int64_t row
 }
 
 template <bool kFromH>
-__global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
+__device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int rows = r.meta[0];
   const int groups = r.inter >> 2;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     r.meta[1] = kFromH ? 1 : 0;
-    if (r.dest.meta_flag != nullptr) *r.dest.meta_flag = r.dest.row_dest != nullptr ? 1 : 0;
+    if (r.dest.meta_flag != nullptr) *r.dest.meta_flag = direct ? 1 : 0;
   }
   for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
     const float w = kFromH ? r.sw.row_weight[row] : 0.0f;
-    const int tok = r.dest.row_dest != nullptr ? r.dest.row_token[row] : 0;
+    const int tok = direct ? r.dest.row_token[row] : 0;
     uint32_t* ar = reinterpret_cast<uint32_t*>(r.act + static_cast<int64_t>(row) * r.inter);
     float m = 0.0f;
     if (groups <= kRequantGroups * kWave) {
@@ -92,7 +94,7 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
         ar[q] = pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
       }
     }
-    if (r.dest.row_dest != nullptr) {
+    if (direct) {
       // the row's token has exactly one routed slot: GEMM2 writes its output row straight to y
       const int slot_row = lane < r.dest.topk
           ? r.dest.output_index[static_cast<int64_t>(tok) * r.dest.topk + lane] : -1;
@@ -103,6 +105,18 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
       r.amax[row] = m;
       r.act_scale[row] = fmaxf(m, kAmaxFloor) / kE4m3Max;
     }
+  }
+}
+
+// kMode 0: from y, 1: from h, 2: decided on the device (a dual GEMM1 launch; RequantArgs)
+template <int kMode>
+__global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
+  if (kMode == 2 && *r.dual_rows >= r.dual_min_rows) {
+    requant_rows<true>(r, r.dest.row_dest != nullptr);
+  } else if (kMode == 2) {
+    requant_rows<false>(r, false);
+  } else {
+    requant_rows<kMode == 1>(r, r.dest.row_dest != nullptr);
   }
 }
 
@@ -299,21 +313,24 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 
 hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw, float* amax,
                           int32_t* meta, uint8_t* act, float* act_scale, int64_t max_rows,
-                          int inter, const RowDest& dest, int num_cus, hipStream_t stream) {
+                          int inter, const RowDest& dest, int num_cus, hipStream_t stream,
+                          const int32_t* dual_rows, int dual_min_rows) {
   if (max_rows <= 0) return hipSuccess;
   if (inter % 4) return hipErrorInvalidValue;
-  if (from_h && sw.row_weight == nullptr) return hipErrorInvalidValue;
+  if ((from_h || dual_rows != nullptr) && sw.row_weight == nullptr) return hipErrorInvalidValue;
   if (dest.row_dest != nullptr && (dest.row_token == nullptr || dest.output_index == nullptr ||
                                    dest.topk < 1 || dest.topk > kWave))
     return hipErrorInvalidValue;
-  const RequantArgs r{src, sw, amax, meta, act, act_scale, inter, dest};
+  const RequantArgs r{src, sw, amax, meta, act, act_scale, inter, dest, dual_rows, dual_min_rows};
   // grid of up to 16 workgroups a CU (one row per wave in flight; the hardware keeps what fits
   // resident): 397 us at 195,558 rows vs 470 us with 4 a CU
   const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 16);
-  if (from_h)
-    hipLaunchKernelGGL(requant_kernel<true>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+  if (dual_rows != nullptr)
+    hipLaunchKernelGGL(requant_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+  else if (from_h)
+    hipLaunchKernelGGL(requant_kernel<1>, dim3(grid), dim3(kEltThreads), 0, stream, r);
   else
-    hipLaunchKernelGGL(requant_kernel<false>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+    hipLaunchKernelGGL(requant_kernel<0>, dim3(grid), dim3(kEltThreads), 0, stream, r);
   return hipGetLastError();
 }
 

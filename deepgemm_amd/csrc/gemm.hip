@@ -1034,6 +1034,11 @@ __device__ __forceinline__ void tile_coords(int local, int cnt, int tile_nb, int
 // kAnyK: K not a multiple of the STREAM chunk (small shapes); the production shapes compile
 // without those variants, which keeps the kernel's code (and its cold instruction fetches in
 // the one-time prologue) smaller.
+// A dual launch's kernel that the routed rows do not select returns at once (GemmArgs).
+__device__ __forceinline__ bool dual_skips(const GemmArgs& g, bool wide) {
+  return g.dual_rows != nullptr && ((*g.dual_rows >= g.dual_min_rows) != wide);
+}
+
 template <bool kGather, bool kSwiglu, bool kAnyK>
 __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1048,11 +1053,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   __shared__ uint8_t s_ev[kFusedMaxTasks];  // in-kernel routing: expert of each task
   __shared__ TileTables s_tt;                // the current item's scales (epilogue)
   const int E = g.num_experts;
-  const bool fused = kSwiglu && g.route_in_kernel;
   const RouteArgs& ra = g.route;
   int ntasks = 0;
-  if (fused) {
+  bool fused = false;
+  if (kSwiglu && g.route_in_kernel) {
     ntasks = effective_tokens(ra.runtime_tokens, ra.host_tokens) * ra.topk;
+    fused = g.route_in_kernel == 1 || ntasks <= kFusedMaxTasks;
+  }
+  // a dual launch: this kernel runs when it routes the live tasks itself (then there are too
+  // few rows for WIDE, and the routed-row count is not written yet), else when the routing's
+  // row count does not select WIDE
+  if (!fused && dual_skips(g, false)) return;
+  if (fused) {
     {  // each wave clears its own count row: only that wave adds to it, so no barrier is needed
       const int wave = static_cast<int>(threadIdx.x) / kWave;
       for (int e = lane_id(); e < E; e += kWave) s_wcnt[wave][e] = 0;
@@ -1164,6 +1176,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 // to the XCDs in contiguous ranges like the 8-wave dispatcher's.
 template <bool kGather, bool kSwiglu, int BM>
 __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wide_gemm_kernel(GemmArgs g) {
+  if (dual_skips(g, true)) return;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ int s_prefix[kMaxGemmExperts + 1];
   __shared__ int s_tile[kMaxGemmExperts];
@@ -1334,20 +1347,45 @@ bool gemm_shape_supported(int n, int k) {
 constexpr int kWideBM1 = 256;
 constexpr int kWideBM2 = 256;
 
-hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream) {
+int gemm_wide_min_rows(int num_experts) {
+  return std::max(kFusedMaxTasks + 1, kWideMinRowsPerExpert * num_experts);
+}
+
+hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream,
+                               const int32_t* rows_on_device, bool route_small_in_kernel) {
   if (max_rows <= 0) return hipSuccess;
-  if (g.num_experts > kMaxGemmExperts) return hipErrorInvalidValue;
+  if (g.num_experts > kMaxGemmExperts || g.dual_rows != nullptr) return hipErrorInvalidValue;
   const bool wide = gemm_wide_selected(g, max_rows);
   if (wide && g.route_in_kernel) return hipErrorInvalidValue;
   // direct writes to y: the WIDE GEMM2 epilogue only
   if (g.y_direct != nullptr && (!wide || g.sw.enabled || g.row_dest == nullptr || g.direct_flag == nullptr))
     return hipErrorInvalidValue;
-  if (g.sw.enabled) {
-    if (g.row_token == nullptr || g.n != 2 * g.sw.inter) return hipErrorInvalidValue;
+  if (g.sw.enabled && (g.row_token == nullptr || g.n != 2 * g.sw.inter)) return hipErrorInvalidValue;
+  if (!g.sw.enabled && g.row_token != nullptr) return hipErrorInvalidValue;
+  if (wide && rows_on_device != nullptr) {
+    // the bound selects WIDE, but the rows are known on the device only: both kernels go out,
+    // and the one the routed rows do not select returns at once (the 8-wave one without the
+    // WIDE GEMM2's direct writes, which the requant then leaves switched off)
+    GemmArgs d = g;
+    d.dual_rows = rows_on_device;
+    d.dual_min_rows = gemm_wide_min_rows(g.num_experts);
+    GemmArgs small = d;
+    small.row_dest = nullptr;
+    small.y_direct = nullptr;
+    small.direct_flag = nullptr;
+    if (route_small_in_kernel) {
+      if (!g.sw.enabled || g.num_experts > kFusedMaxExperts) return hipErrorInvalidValue;
+      small.route_in_kernel = 2;
+    }
+    const hipError_t err = g.sw.enabled ? launch_engines<true, true>(small, max_rows, num_cus, stream)
+                                        : launch_engines<false, false>(small, max_rows, num_cus, stream);
+    if (err != hipSuccess) return err;
+    return g.sw.enabled ? launch_wide<true, true, kWideBM1>(d, max_rows, num_cus, stream)
+                        : launch_wide<false, false, kWideBM2>(d, max_rows, num_cus, stream);
+  }
+  if (g.sw.enabled)
     return wide ? launch_wide<true, true, kWideBM1>(g, max_rows, num_cus, stream)
                 : launch_engines<true, true>(g, max_rows, num_cus, stream);
-  }
-  if (g.row_token != nullptr) return hipErrorInvalidValue;
   return wide ? launch_wide<false, false, kWideBM2>(g, max_rows, num_cus, stream)
               : launch_engines<false, false>(g, max_rows, num_cus, stream);
 }

@@ -31,6 +31,8 @@ struct RouteArgs {
   int32_t* m_indices;             // [rows] or null
   int32_t* zero_ints;             // zeroed by the routing launch (the GEMMs' claim counters), or null
   int zero_count;
+  int64_t fused_max_tasks;        // > 0: the launch returns at once when the live tasks are at
+                                  // most this many (GEMM1 then routes them in-kernel)
 };
 
 // Count -> offsets -> stable scatter over at most max_tasks = S*K tasks. Deterministic: rows
@@ -67,7 +69,8 @@ struct GemmArgs {
   int k;
   GemmEngine engine;
   SwigluEpilogue sw;         // GEMM1 only (requires row_token); c is unused then
-  int route_in_kernel;       // GEMM1: route the tasks in the kernel (<= gemm_route_max_tasks())
+  int route_in_kernel;       // GEMM1: 1 = route the tasks in the kernel (<= gemm_route_max_tasks()),
+                             // 2 = only when the live tasks are at most that many
   RouteArgs route;           // the routing to do then (counts, offsets, row tables are written)
   // GEMM2 on the WIDE kernel, when *direct_flag != 0: rows with row_dest[r] >= 0 go to
   // y_direct[row_dest[r]] (bf16 [S, N], a negative zero stored as +0 like the combine's sum)
@@ -78,13 +81,28 @@ struct GemmArgs {
   // WIDE kernel work claiming (kSchedInts ints, zero at launch; the kernel leaves them zero):
   // [0..7] per-XCD claim counters, [8] finished workgroups. Null: static dealing.
   int32_t* sched;
+  // Set by launch_grouped_gemm for a row bound that selects the WIDE kernel while the actual rows
+  // are only known on the device (graph replays): the 8-wave and the WIDE kernel are both
+  // launched, and each returns at once unless the routed rows (*dual_rows, the routing's
+  // meta[0]) select it -- WIDE at dual_min_rows or more. Null: the launch always runs.
+  const int32_t* dual_rows;
+  int dual_min_rows;
 };
 constexpr int kSchedInts = 16;
 
 // Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
 // a_scale[r] * b_scale[e,n]). Persistent: the grid strides over the tiles, enumerated on the
-// device from counts (max_rows bounds the grid only).
-hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream);
+// device from counts (max_rows bounds the grid only). With rows_on_device (the routing's
+// meta[0]) and a bound that selects the WIDE kernel, the kernel is chosen on the device from
+// the routed rows instead (GemmArgs::dual_rows).
+// In such a dual GEMM1 launch with route_small_in_kernel, the 8-wave kernel also routes the tasks
+// itself when the live ones fit (route_in_kernel 2; the routing launch then returns at once:
+// RouteArgs::fused_max_tasks).
+hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream,
+                               const int32_t* rows_on_device = nullptr,
+                               bool route_small_in_kernel = false);
+// The routed-row count from which the WIDE kernel is chosen on the device (dual launches).
+int gemm_wide_min_rows(int num_experts);
 bool gemm_shape_supported(int n, int k);
 // True when launch_grouped_gemm runs the WIDE kernel for g: GEMM1 then writes the bf16
 // pre-activation h [rows, 2I] instead of the SwiGLU output y (requant computes the SwiGLU).
@@ -110,9 +128,13 @@ struct RowDest {
 // SwiGLU output, or with from_h the SwiGLU of GEMM1's bf16 pre-activation h [rows, 2I]
 // computed here (sw: route weights and clamp). meta[1] records which (1 = from h). With
 // dest.row_dest it also builds the direct-write table (RowDest).
+// With dual_rows (a dual GEMM1 launch): from_h is decided on the device, true when
+// *dual_rows >= dual_min_rows (the WIDE GEMM1 ran), and the direct-write table is built only
+// then.
 hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw, float* amax,
                           int32_t* meta, uint8_t* act, float* act_scale, int64_t max_rows,
-                          int inter, const RowDest& dest, int num_cus, hipStream_t stream);
+                          int inter, const RowDest& dest, int num_cus, hipStream_t stream,
+                          const int32_t* dual_rows = nullptr, int dual_min_rows = 0);
 
 struct CombineArgs {
   uint16_t* y;                     // bf16 [S, H]

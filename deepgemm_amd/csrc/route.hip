@@ -102,6 +102,12 @@ __device__ void publish_offsets(const RouteArgs& a, const int* s_tot, int* s_off
   }
 }
 
+// A routing launch that GEMM1 stands in for (the live tasks fit its in-kernel routing).
+__device__ __forceinline__ bool route_skipped(const RouteArgs& a) {
+  return a.fused_max_tasks > 0 &&
+         static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk <= a.fused_max_tasks;
+}
+
 // The routing launch runs before the GEMMs of a layer: it zeroes their claim counters.
 __device__ __forceinline__ void zero_sched(const RouteArgs& a) {
   if (blockIdx.x == 0 && a.zero_ints != nullptr)
@@ -109,6 +115,7 @@ __device__ __forceinline__ void zero_sched(const RouteArgs& a) {
 }
 
 __global__ __launch_bounds__(kSmallThreads) void route_small_kernel(RouteArgs a) {
+  if (route_skipped(a)) return;
   zero_sched(a);
   __shared__ int s_cnt[kSmallWaves][kSmallMaxExperts];
   __shared__ int s_tot[kSmallMaxExperts];
@@ -142,6 +149,7 @@ __global__ __launch_bounds__(kSmallThreads) void route_small_kernel(RouteArgs a)
 
 __global__ __launch_bounds__(kChunkThreads) void route_count_kernel(RouteArgs a, int chunk_tasks) {
   __shared__ int s_cnt[kMaxExperts];
+  if (route_skipped(a)) return;
   zero_sched(a);
   const int tid = threadIdx.x;
   for (int e = tid; e < a.num_experts; e += kChunkThreads) s_cnt[e] = 0;
@@ -166,6 +174,7 @@ __global__ __launch_bounds__(kChunkThreads) void route_count_kernel(RouteArgs a,
 __global__ __launch_bounds__(kChunkThreads) void route_chunk_scatter_kernel(RouteArgs a,
                                                                             int chunk_tasks,
                                                                             int num_chunks) {
+  if (route_skipped(a)) return;
   __shared__ int s_wbase[kChunkWaves][kMaxExperts];
   __shared__ int s_tot[kMaxExperts];
   __shared__ int s_off[kMaxExperts + 1];

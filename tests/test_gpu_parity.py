@@ -524,15 +524,17 @@ def test_layer_no_routed_rows(mm, cuda):
 
 # ------------------------------------------------------------------ graph-bucket mode
 @pytest.mark.parametrize("flag", ["big_fused_cuda_graph", "stages_fused_cuda_graph"])
-@pytest.mark.parametrize("bucket", [(200, 8), (2048, 4)])
+@pytest.mark.parametrize("bucket", [(200, 8, 16), (2048, 4, 16), (3000, 8, None)])
 def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
     """Capture once at the bucket size, replay with several device token counts: every replay
     equals an eager call on that prefix (bitwise) and leaves rows past the prefix untouched.
-    The 2048-token bucket is captured with the 4-wave WIDE GEMMs; the eager calls on the short
-    prefixes run the 8-wave kernels (same sums in the same order, so the same bits)."""
-    s_max, e = bucket
+    The large buckets' row bound selects the 4-wave WIDE GEMMs, so both those and the 8-wave
+    kernels are captured and the routed rows choose on the device: WIDE from
+    max(8193, 256 * E) rows (the 3000-token bucket's full replays), the 8-wave kernels below
+    (short prefixes) -- the same sums in the same order either way, so the same bits."""
+    s_max, e, g = bucket
     hdim, inter, k = 512, 256, 6
-    x_fp8, x_sf, idx, w = make_tokens(s_max, hdim, e, k, seed=21, global_experts=16)
+    x_fp8, x_sf, idx, w = make_tokens(s_max, hdim, e, k, seed=21, global_experts=g)
     l1, l2 = make_weights_gpu(e, hdim, inter, seed=22, mm=mm)
     buf = mm.get_symm_buffer_for_mega_moe(None, e, s_max, k, hdim, inter)
     for t, src in ((buf.x, x_fp8), (buf.x_sf, x_sf), (buf.topk_idx, idx), (buf.topk_weights, w)):
@@ -545,17 +547,28 @@ def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
     with torch.cuda.graph(graph):
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf, **{flag: True})
     ref_buf = mm.SymmBuffer(None, e, s_max, k, hdim, inter)
+    wide_min = max(8193, 256 * e)
+    kinds = set()
     for n in (s_max, 57, 1, 0, 133, s_max - 77):
         log(f"  replay with runtime tokens={n}")
         y.fill_(7.0)
         buf.cuda_graph_num_tokens.fill_(n)
         graph.replay()
         torch.cuda.synchronize()
+        meta = buf.scratch_view("meta").cpu()
+        live_ids = idx[:n]
+        routed = int(((live_ids >= 0) & (live_ids < e) & (w[:n] != 0)).sum())
+        assert int(meta[0].item()) == routed, f"n={n}: routed rows of this replay"
+        wide = bool(meta[1].item() == 1)
+        assert wide == (routed >= wide_min), f"n={n}: kernel choice for R={routed}"
+        kinds.add(wide)
         if n > 0:
             y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2)
             torch.cuda.synchronize()
             assert torch.equal(y[:n], y_ref), f"replay n={n}"
         assert torch.all(y[n:] == 7.0), f"rows past the prefix were written (n={n})"
+    if g is None:  # every slot local: the full replays run WIDE, the short ones the 8-wave kernels
+        assert kinds == {True, False}
 
 
 # ------------------------------------------------------------------ pre/post-process
