@@ -1362,6 +1362,13 @@ hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hip
     return hipErrorInvalidValue;
   if (g.sw.enabled && (g.row_token == nullptr || g.n != 2 * g.sw.inter)) return hipErrorInvalidValue;
   if (!g.sw.enabled && g.row_token != nullptr) return hipErrorInvalidValue;
+  // the 8-wave kernel routes the live tasks itself when they fit (the routing launch of the
+  // same call returns at once then): a GEMM1 on device-read tokens only
+  if (route_small_in_kernel && (!g.sw.enabled || g.route_in_kernel || rows_on_device == nullptr ||
+                                g.num_experts > kFusedMaxExperts))
+    return hipErrorInvalidValue;
+  GemmArgs eight = g;
+  if (route_small_in_kernel) eight.route_in_kernel = 2;
   if (wide && rows_on_device != nullptr) {
     // the bound selects WIDE, but the rows are known on the device only: both kernels go out,
     // and the one the routed rows do not select returns at once (the 8-wave one without the
@@ -1369,25 +1376,23 @@ hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hip
     GemmArgs d = g;
     d.dual_rows = rows_on_device;
     d.dual_min_rows = gemm_wide_min_rows(g.num_experts);
-    GemmArgs small = d;
-    small.row_dest = nullptr;
-    small.y_direct = nullptr;
-    small.direct_flag = nullptr;
-    if (route_small_in_kernel) {
-      if (!g.sw.enabled || g.num_experts > kFusedMaxExperts) return hipErrorInvalidValue;
-      small.route_in_kernel = 2;
-    }
-    const hipError_t err = g.sw.enabled ? launch_engines<true, true>(small, max_rows, num_cus, stream)
-                                        : launch_engines<false, false>(small, max_rows, num_cus, stream);
+    eight.dual_rows = d.dual_rows;
+    eight.dual_min_rows = d.dual_min_rows;
+    eight.row_dest = nullptr;
+    eight.y_direct = nullptr;
+    eight.direct_flag = nullptr;
+    const hipError_t err = g.sw.enabled ? launch_engines<true, true>(eight, max_rows, num_cus, stream)
+                                        : launch_engines<false, false>(eight, max_rows, num_cus, stream);
     if (err != hipSuccess) return err;
     return g.sw.enabled ? launch_wide<true, true, kWideBM1>(d, max_rows, num_cus, stream)
                         : launch_wide<false, false, kWideBM2>(d, max_rows, num_cus, stream);
   }
+  if (wide && route_small_in_kernel) return hipErrorInvalidValue;  // (rows_on_device is set)
   if (g.sw.enabled)
     return wide ? launch_wide<true, true, kWideBM1>(g, max_rows, num_cus, stream)
-                : launch_engines<true, true>(g, max_rows, num_cus, stream);
+                : launch_engines<true, true>(eight, max_rows, num_cus, stream);
   return wide ? launch_wide<false, false, kWideBM2>(g, max_rows, num_cus, stream)
-              : launch_engines<false, false>(g, max_rows, num_cus, stream);
+              : launch_engines<false, false>(eight, max_rows, num_cus, stream);
 }
 
 }  // namespace mmoe

@@ -95,9 +95,10 @@ constexpr int kSchedInts = 16;
 // device from counts (max_rows bounds the grid only). With rows_on_device (the routing's
 // meta[0]) and a bound that selects the WIDE kernel, the kernel is chosen on the device from
 // the routed rows instead (GemmArgs::dual_rows).
-// In such a dual GEMM1 launch with route_small_in_kernel, the 8-wave kernel also routes the tasks
-// itself when the live ones fit (route_in_kernel 2; the routing launch then returns at once:
-// RouteArgs::fused_max_tasks).
+// With route_small_in_kernel (a GEMM1 on device-read tokens whose bound is too large for
+// in-kernel routing), the 8-wave kernel routes the tasks itself when the live ones fit
+// (route_in_kernel 2); the call's routing launch then returns at once
+// (RouteArgs::fused_max_tasks).
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream,
                                const int32_t* rows_on_device = nullptr,
                                bool route_small_in_kernel = false);

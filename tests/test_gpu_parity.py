@@ -524,14 +524,16 @@ def test_layer_no_routed_rows(mm, cuda):
 
 # ------------------------------------------------------------------ graph-bucket mode
 @pytest.mark.parametrize("flag", ["big_fused_cuda_graph", "stages_fused_cuda_graph"])
-@pytest.mark.parametrize("bucket", [(200, 8, 16), (2048, 4, 16), (3000, 8, None)])
+@pytest.mark.parametrize("bucket", [(200, 8, 16), (2048, 4, 16), (3000, 8, None), (2000, 64, None)])
 def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
     """Capture once at the bucket size, replay with several device token counts: every replay
     equals an eager call on that prefix (bitwise) and leaves rows past the prefix untouched.
     The large buckets' row bound selects the 4-wave WIDE GEMMs, so both those and the 8-wave
     kernels are captured and the routed rows choose on the device: WIDE from
     max(8193, 256 * E) rows (the 3000-token bucket's full replays), the 8-wave kernels below
-    (short prefixes) -- the same sums in the same order either way, so the same bits."""
+    (short prefixes) -- the same sums in the same order either way, so the same bits. Buckets
+    of more than 8192 tasks also leave the routing to GEMM1 when the live tasks fit in it; the
+    64-expert bucket does so without selecting WIDE (fewer than 256 rows per expert)."""
     s_max, e, g = bucket
     hdim, inter, k = 512, 256, 6
     x_fp8, x_sf, idx, w = make_tokens(s_max, hdim, e, k, seed=21, global_experts=g)
@@ -567,8 +569,9 @@ def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
             torch.cuda.synchronize()
             assert torch.equal(y[:n], y_ref), f"replay n={n}"
         assert torch.all(y[n:] == 7.0), f"rows past the prefix were written (n={n})"
-    if g is None:  # every slot local: the full replays run WIDE, the short ones the 8-wave kernels
-        assert kinds == {True, False}
+    if g is None:  # every slot local: the full replays run WIDE (if the rows select it) and the
+        # short ones the 8-wave kernels
+        assert kinds == ({True, False} if s_max * k >= wide_min else {False})
 
 
 # ------------------------------------------------------------------ pre/post-process
