@@ -637,9 +637,11 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
         if (grow < mrows) *reinterpret_cast<int4*>(out + grow * ld) = val[i];
       } else {
         // the row's address from the table (its part row or its token's y row); a global (not
-        // flat) store: a flat one would also hold up the LDS counter
+        // flat) store: a flat one would also hold up the LDS counter. Nontemporal: the rows are
+        // read once, by the combine (c3 -25 us; the same hint on GEMM1's h stores was slower)
         const i32x4 v = {val[i].x, val[i].y, val[i].z, val[i].w};
-        if (grow < mrows) *(__attribute__((address_space(1))) i32x4*)(base[i] + col * 2) = v;
+        if (grow < mrows)
+          __builtin_nontemporal_store(v, (__attribute__((address_space(1))) i32x4*)(base[i] + col * 2));
       }
     }
     // the next pass's LDS writes follow these reads in the wave's own (in-order) LDS queue
