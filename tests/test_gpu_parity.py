@@ -574,6 +574,38 @@ def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
         assert kinds == ({True, False} if s_max * k >= wide_min else {False})
 
 
+def test_graph_full_shape_both_kernels(mm, cuda, full_weights):
+    """The production shape in a 2048-token bucket (every slot local: a WIDE row bound): a full
+    replay runs the WIDE kernels, a short one the 8-wave kernels with GEMM1 routing in-kernel;
+    both are bitwise equal to eager calls on the same prefix."""
+    l1, l2 = full_weights[0], full_weights[1]
+    s_max = 2048
+    x_fp8, x_sf, idx, w = make_tokens(s_max, 4096, 32, 6, seed=333, global_experts=None)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    for t, src in ((buf.x, x_fp8), (buf.x_sf, x_sf), (buf.topk_idx, idx), (buf.topk_weights, w)):
+        t[:s_max].copy_(src)
+    y = torch.zeros((s_max, 4096), dtype=torch.bfloat16, device=cuda)
+    log("full-shape graph: warm-up and capture at 2048 tokens")
+    mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
+    ref_buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    for n, wide in ((s_max, True), (100, False)):
+        log(f"  replay with runtime tokens={n}")
+        y.fill_(7.0)
+        buf.cuda_graph_num_tokens.fill_(n)
+        graph.replay()
+        torch.cuda.synchronize()
+        meta = buf.scratch_view("meta").cpu()
+        assert int(meta[0]) == 6 * n and bool(meta[1] == 1) == wide, f"n={n}: kernel choice"
+        y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2)
+        torch.cuda.synchronize()
+        assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
+        assert torch.all(y[n:] == 7.0)
+
+
 # ------------------------------------------------------------------ pre/post-process
 @pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
 def test_deepep_pre_post_process(mm, cuda, ids_dtype):
