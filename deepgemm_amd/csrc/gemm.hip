@@ -230,6 +230,14 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[
 }
 
 // ------------------------------------------------------------------ STREAM engine
+// The 8 waves of a STREAM tile step together: a bare s_barrier after every 64-k step (each wave
+// has issued that step's ring refill before it, so the weight loads stay in flight). Left to
+// themselves the waves drift apart -- the memory pipeline does not serve them evenly -- and a
+// workgroup's first and last wave finished their streams 15-16 us apart at c1 (median), the
+// last one 6-7 us after the median one, with fewer and fewer loads in flight at the end. In
+// step, GEMM1 went from 109 to 97 us at c1 (a barrier every 4 steps: 103 us).
+__device__ __forceinline__ void step_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 // Workgroup barrier for the LDS A chunks: this wave's LDS writes are complete, then s_barrier.
 // It waits on no global load, so the weight loads in flight stay in flight.
 __device__ __forceinline__ void lds_barrier() {
@@ -356,6 +364,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
         compute(d, c, j + d);
         issue(d, c * spc + j + d + D);
         __builtin_amdgcn_sched_barrier(0);
+        if (kFast) step_barrier();
       }
     }
     store_chunk(c + 1);  // its buffer was last read in chunk c - 1, before the last barrier
@@ -369,6 +378,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
         compute(d, c, j + d);
         issue(d, c * spc + j + d + D);
         __builtin_amdgcn_sched_barrier(0);
+        if (kFast) step_barrier();
       }
     }
 #pragma unroll
