@@ -32,22 +32,33 @@ __device__ __forceinline__ int expert_id_bits(int num_experts) {
 }
 
 // Loads P passes of 64 tasks starting at `begin` (task begin + p*64 + lane) into registers,
-// all loads issued before any is used (one memory round trip per batch).
-template <int P>
-__device__ __forceinline__ void wave_load(const RouteArgs& a, int64_t begin, int64_t end, int* ev,
-                                          float* wv) {
+// all loads issued before any is used (one memory round trip per batch). The id width is a
+// branch around the whole batch: a width test per load placed a wait inside every branch, and
+// the batch's loads went out one round trip at a time.
+template <int P, typename Id>
+__device__ __forceinline__ void wave_load_ids(const Id* idx, const float* topk_w, int64_t begin,
+                                              int64_t end, int64_t* ids, float* wv) {
   const int lane = lane_id();
-  int64_t ids[P];
+  Id raw[P];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int64_t task = begin + p * kWave + lane;
-    const bool ok = task < end;
-    const int64_t t = ok ? task : 0;
-    ids[p] = a.idx_i64 ? static_cast<const int64_t*>(a.topk_idx)[t]
-                       : static_cast<int64_t>(static_cast<const int32_t*>(a.topk_idx)[t]);
-    wv[p] = a.topk_w[t];
-    if (!ok) ids[p] = -1;
+    const int64_t t = task < end ? task : 0;
+    raw[p] = idx[t];
+    wv[p] = topk_w[t];
   }
+#pragma unroll
+  for (int p = 0; p < P; ++p) ids[p] = begin + p * kWave + lane < end ? static_cast<int64_t>(raw[p]) : -1;
+}
+
+template <int P>
+__device__ __forceinline__ void wave_load(const RouteArgs& a, int64_t begin, int64_t end, int* ev,
+                                          float* wv) {
+  int64_t ids[P];
+  if (a.idx_i64)
+    wave_load_ids<P>(static_cast<const int64_t*>(a.topk_idx), a.topk_w, begin, end, ids, wv);
+  else
+    wave_load_ids<P>(static_cast<const int32_t*>(a.topk_idx), a.topk_w, begin, end, ids, wv);
 #pragma unroll
   for (int p = 0; p < P; ++p) ev[p] = valid_expert(a, ids[p], wv[p]);
 }
