@@ -74,6 +74,20 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (all lanes active), by DPP: row shifts 1, 2,
+// 4, 8 within each 16-lane row (a lane without a source adds 0), then row 0's total into row 1
+// and row 2's into row 3 (row_bcast:15), then rows 0-1's total into rows 2 and 3 (row_bcast:31).
+// Six dependent VALU steps, no LDS permutes.
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15, rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31, rows 2 and 3
+  return v;
+}
+
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);

@@ -838,7 +838,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
 constexpr int kFusedPasses = 16;  // 64-task passes per wave
 constexpr int kFusedMaxTasks = kGemmWaves * kFusedPasses * kWave;
 constexpr int kFusedMaxExperts = 255;  // expert ids in a byte, 255 = invalid task
-constexpr int kFusedBatch = 8;         // passes whose loads are in flight together
+constexpr int kFusedBatch = 16;        // passes whose loads are in flight together
 constexpr int kRowTable = kTileBM;  // LDS row table: one TILE's 256 rows
 
 __device__ __forceinline__ int fused_per_wave(int ntasks) {
@@ -946,12 +946,7 @@ __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const 
                      : (cnt + kStreamRows - 1) / kStreamRows * stream_nb;
         s_tile[e] = tile;
       }
-      int inc = items;
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const int u = __shfl_up(inc, off, kWave);
-        if (lane >= off) inc += u;
-      }
+      const int inc = wave_inclusive_sum(items);
       if (e < E) s_prefix[e] = carry + inc - items;
       carry += __shfl(inc, kWave - 1, kWave);
     }
@@ -1100,12 +1095,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
           }
           s_count[e] = run;
         }
-        int inc = run;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-          const int u = __shfl_up(inc, off, kWave);
-          if (lane >= off) inc += u;
-        }
+        const int inc = wave_inclusive_sum(run);
         if (e < E) s_off[e] = carry + inc - run;
         carry += __shfl(inc, kWave - 1, kWave);
       }
