@@ -88,12 +88,6 @@ __device__ __forceinline__ int wave_inclusive_sum(int v) {
   return v;
 }
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
-
 __device__ __forceinline__ int lane_id() { return static_cast<int>(threadIdx.x) & (kWave - 1); }
 
 // Number of tokens this call processes: the device scalar (clamped to [0, cap]) when given,
