@@ -201,6 +201,10 @@ def _combine_bitwise(mm, buf, y, l1, l2, s, clamp):
     (1500, 5, 768, 256, 6, 8, None),
     # >= 16 tokens a CU: the whole-row combine; most tokens have one routed slot (direct rows)
     (4500, 4, 256, 256, 2, 16, None),
+    # GEMM1's in-kernel routing over more than one 64-expert scan chunk (S*K <= 8192), up to
+    # its largest expert count (255: expert ids in a byte)
+    (512, 160, 256, 128, 8, None, None),
+    (300, 255, 256, 128, 6, None, None),
 ])
 def test_layer_small_shapes(mm, cuda, cfg):
     s, e, hdim, inter, k, g, clamp = cfg
