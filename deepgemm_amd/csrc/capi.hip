@@ -48,7 +48,7 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->counts_offset = take(e_local * 4);
   l->offsets_offset = take((e_local + 1) * 4);
   l->meta_offset = take(16 * 4);
-  l->chunk_counts_offset = take((chunks > 0 ? chunks : 1) * e_local * 4);
+  l->chunk_counts_offset = take(mmoe::route_count_ints(tasks, static_cast<int>(e_local)) * 4);
   l->output_index_offset = take((tasks > 0 ? tasks : 1) * 4);
   l->row_token_offset = take(rows * 4);
   l->row_weight_offset = take(rows * 4);
@@ -150,6 +150,7 @@ mmoe::RouteArgs forward_route_args(const mmoe_forward_args* a, const mmoe_scratc
   r.check_weight = 1;
   r.row_cap = l.row_capacity;
   r.chunk_counts = at<int32_t>(ws, l.chunk_counts_offset);
+  r.wave_counts = r.chunk_counts + (l.num_chunks > 0 ? l.num_chunks : 1) * a->num_experts;
   r.counts = at<int32_t>(ws, l.counts_offset);
   r.offsets = at<int32_t>(ws, l.offsets_offset);
   r.meta = at<int32_t>(ws, l.meta_offset);
@@ -463,7 +464,7 @@ int mmoe_deepep_preprocess_workspace_bytes(int recv_rows, int topk, int num_expe
   off = align_up(off + num_experts * 4, 256);            // counts
   off = align_up(off + (num_experts + 1) * 4, 256);      // offsets
   off = align_up(off + 16 * 4, 256);                     // meta
-  off = align_up(off + (chunks > 0 ? chunks : 1) * num_experts * 4, 256);
+  off = align_up(off + mmoe::route_count_ints(tasks, num_experts) * 4, 256);  // chunk, wave counts
   off = align_up(off + (total_rows > 0 ? total_rows : 1) * 4, 256);  // row_token
   *out_bytes = off;
   return MMOE_OK;
@@ -502,7 +503,8 @@ int mmoe_deepep_preprocess_channelwise(void* grouped_x, float* grouped_x_scale,
   r.counts = at<int32_t>(workspace, take(num_experts * 4));
   r.offsets = at<int32_t>(workspace, take((num_experts + 1) * 4));
   r.meta = at<int32_t>(workspace, take(16 * 4));
-  r.chunk_counts = at<int32_t>(workspace, take(chunks * num_experts * 4));
+  r.chunk_counts = at<int32_t>(workspace, take(mmoe::route_count_ints(tasks, num_experts) * 4));
+  r.wave_counts = r.chunk_counts + (chunks > 0 ? chunks : 1) * num_experts;
   r.row_token = at<int32_t>(workspace, take((total_rows > 0 ? total_rows : 1) * 4));
   r.topk_idx = recv_topk_ids;
   r.idx_i64 = topk_ids_i64 ? 1 : 0;

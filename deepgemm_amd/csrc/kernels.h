@@ -7,6 +7,7 @@
 namespace mmoe {
 
 constexpr int kRouteChunk = 1024;  // tasks per routing chunk (== MMOE_ROUTE_CHUNK)
+constexpr int kRouteWaves = 16;    // waves of a routing chunk's workgroup
 constexpr int kMaxExperts = 1024;  // LDS-resident per-expert tables in the routing kernels
 
 struct RouteArgs {
@@ -20,6 +21,8 @@ struct RouteArgs {
   int check_weight;               // forward rule: w != 0 required
   int64_t row_cap;                // rows >= row_cap are dropped (output_index = -1)
   int32_t* chunk_counts;          // [nchunks, E] per-chunk counts (large launches only)
+  int32_t* wave_counts;           // [nchunks, kRouteWaves, E] per-wave counts of each chunk
+                                  // (large launches), or null: the scatter counts again
   int32_t* counts;                // [E]
   int32_t* offsets;               // [E+1]
   int32_t* meta;                  // [16]; meta[0] = R
@@ -36,8 +39,13 @@ struct RouteArgs {
 };
 
 // Count -> offsets -> stable scatter over at most max_tasks = S*K tasks. Deterministic: rows
-// of an expert in ascending task order. chunk_counts needs ceil(max_tasks/kRouteChunk)*E ints.
+// of an expert in ascending task order. chunk_counts needs ceil(max_tasks/kRouteChunk)*E ints,
+// wave_counts kRouteWaves times as many (route_count_ints gives both together).
 hipError_t launch_route(const RouteArgs& a, int64_t max_tasks, hipStream_t stream);
+inline int64_t route_count_ints(int64_t max_tasks, int num_experts) {
+  const int64_t chunks = (max_tasks + kRouteChunk - 1) / kRouteChunk;
+  return (chunks > 0 ? chunks : 1) * num_experts * (1 + kRouteWaves);
+}
 
 // Per-expert tile engine of the grouped GEMM: kAuto picks STREAM for experts with <= 64 rows
 // (weight streaming, decode) and TILE otherwise (256x256 MFMA tiles, prefill).

@@ -31,6 +31,7 @@ constexpr int kChunkThreads = 1024;
 constexpr int kChunkWaves = kChunkThreads / kWave;
 static_assert(kMaxExperts <= kChunkThreads, "the chunk-count reduction needs a thread per expert");
 static_assert(2 * kChunkThreads <= kChunkWaves * kMaxExperts, "partial sums fit in s_wbase");
+static_assert(kChunkWaves == kRouteWaves, "per-wave counts of a chunk in the workspace");
 
 // Assigns rows to one 64-task pass in task order; base[e] is this wave's running base.
 __device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t task, bool in_range,
@@ -55,9 +56,8 @@ __device__ __forceinline__ void wave_scatter_pass(const RouteArgs& a, int64_t ta
 // the caller turns counts into bases (needs a workgroup barrier), passed through `phase_gap`.
 constexpr int kBatch = 8;
 
-template <class Gap>
-__device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* row,
-                           Gap phase_gap) {
+// Counts of the tasks [begin, end) of this wave into its count row.
+__device__ void wave_count_range(const RouteArgs& a, int64_t begin, int64_t end, int* row) {
   int ev[kBatch];
   float wv[kBatch];
   const int id_bits = expert_id_bits(a.num_experts);
@@ -66,6 +66,16 @@ __device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* 
 #pragma unroll
     for (int p = 0; p < kBatch; ++p) wave_count_pass(ev[p], id_bits, row);
   }
+}
+
+// counted: the count rows hold this range's counts already (the count kernel's).
+template <class Gap>
+__device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* row,
+                           Gap phase_gap, bool counted = false) {
+  int ev[kBatch];
+  float wv[kBatch];
+  const int id_bits = expert_id_bits(a.num_experts);
+  if (!counted) wave_count_range(a, begin, end, row);
   phase_gap();
   const int lane = lane_id();
   for (int64_t b = begin; b < end; b += kBatch * kWave) {
@@ -78,19 +88,26 @@ __device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* 
   }
 }
 
-// Expert offsets from totals (exclusive scan, or the caller's counts for the preprocess),
-// written by one thread; returns nothing, fills s_off[0..E].
+// Expert offsets from totals (exclusive scan, or the caller's counts for the preprocess), by
+// wave 0 in 64-expert chunks (DPP scans); fills s_off[0..E], and the writer workgroup
+// publishes offsets, counts, stats and the routed row count.
 __device__ void publish_offsets(const RouteArgs& a, const int* s_tot, int* s_off, bool writer) {
-  if (threadIdx.x == 0) {
-    int64_t off = 0;
-    int64_t routed = 0;
-    for (int e = 0; e < a.num_experts; ++e) {
-      s_off[e] = static_cast<int>(off);
-      off += a.given_counts != nullptr ? a.given_counts[e] : s_tot[e];
-      routed += s_tot[e];
+  if (threadIdx.x < kWave) {
+    const int lane = lane_id();
+    int carry = 0, routed = 0;
+    for (int e0 = 0; e0 < a.num_experts; e0 += kWave) {
+      const int e = e0 + lane;
+      const int tot = e < a.num_experts ? s_tot[e] : 0;
+      const int c = a.given_counts != nullptr ? (e < a.num_experts ? a.given_counts[e] : 0) : tot;
+      const int inc = wave_inclusive_sum(c);
+      if (e < a.num_experts) s_off[e] = carry + inc - c;
+      carry += __shfl(inc, kWave - 1, kWave);
+      routed += __shfl(wave_inclusive_sum(tot), kWave - 1, kWave);
     }
-    s_off[a.num_experts] = static_cast<int>(off);
-    if (writer) a.meta[0] = static_cast<int32_t>(routed < a.row_cap ? routed : a.row_cap);
+    if (lane == 0) {
+      s_off[a.num_experts] = carry;
+      if (writer) a.meta[0] = static_cast<int32_t>(routed < a.row_cap ? routed : a.row_cap);
+    }
   }
   __syncthreads();
   if (writer) {
@@ -147,29 +164,48 @@ __global__ __launch_bounds__(kSmallThreads) void route_small_kernel(RouteArgs a)
   });
 }
 
+// The tasks of chunk `chunk` that wave `wave` of a chunk workgroup routes: the same split in
+// the count and the scatter kernels, so the scatter can take the count kernel's per-wave counts.
+struct WaveRange {
+  int64_t begin, end;
+};
+__device__ __forceinline__ WaveRange chunk_wave_range(int64_t ntasks, int chunk, int chunk_tasks, int wave) {
+  const int64_t cbegin = static_cast<int64_t>(chunk) * chunk_tasks;
+  const int64_t cend = cbegin + chunk_tasks < ntasks ? cbegin + chunk_tasks : ntasks;
+  const int64_t per = ((chunk_tasks / kChunkWaves) + kWave - 1) / kWave * kWave;
+  const int64_t begin = cbegin + wave * per < cend ? cbegin + wave * per : cend;
+  return WaveRange{begin, begin + per < cend ? begin + per : cend};
+}
+
+// Per-wave counts of a chunk (each wave's ballot counts of its own task range, no atomics);
+// writes the chunk's totals and, when wave_counts is given, the per-wave rows.
 __global__ __launch_bounds__(kChunkThreads) void route_count_kernel(RouteArgs a, int chunk_tasks) {
-  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_cnt[kChunkWaves][kMaxExperts];
   if (route_skipped(a)) return;
   zero_sched(a);
   const int tid = threadIdx.x;
-  for (int e = tid; e < a.num_experts; e += kChunkThreads) s_cnt[e] = 0;
+  const int wave = tid / kWave;
+  const int E = a.num_experts;
+  for (int i = tid; i < kChunkWaves * E; i += kChunkThreads) s_cnt[i / E][i % E] = 0;
   __syncthreads();
   const int64_t ntasks =
       static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * chunk_tasks;
-  for (int i = tid; i < chunk_tasks; i += kChunkThreads) {
-    const int64_t task = base + i;
-    if (task < ntasks) {
-      const int64_t id = a.idx_i64 ? static_cast<const int64_t*>(a.topk_idx)[task]
-                                   : static_cast<const int32_t*>(a.topk_idx)[task];
-      const int e = valid_expert(a, id, a.topk_w[task]);
-      if (e >= 0) atomicAdd(&s_cnt[e], 1);
-    }
-  }
+  const WaveRange wr = chunk_wave_range(ntasks, blockIdx.x, chunk_tasks, wave);
+  wave_count_range(a, wr.begin, wr.end, s_cnt[wave]);
   __syncthreads();
-  int32_t* dst = a.chunk_counts + static_cast<int64_t>(blockIdx.x) * a.num_experts;
-  for (int e = tid; e < a.num_experts; e += kChunkThreads) dst[e] = s_cnt[e];
+  int32_t* dst = a.chunk_counts + static_cast<int64_t>(blockIdx.x) * E;
+  for (int e = tid; e < E; e += kChunkThreads) {
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < kChunkWaves; ++w) tot += s_cnt[w][e];
+    dst[e] = tot;
+  }
+  if (a.wave_counts != nullptr) {
+    int32_t* wdst = a.wave_counts + static_cast<int64_t>(blockIdx.x) * kChunkWaves * E;
+    for (int i = tid; i < kChunkWaves * E; i += kChunkThreads) wdst[i] = s_cnt[i / E][i % E];
+  }
 }
+
 
 __global__ __launch_bounds__(kChunkThreads) void route_chunk_scatter_kernel(RouteArgs a,
                                                                             int chunk_tasks,
@@ -194,7 +230,18 @@ __global__ __launch_bounds__(kChunkThreads) void route_chunk_scatter_kernel(Rout
     if (tid < groups * E) {
       const int e = tid % E, g = tid / E;
       int tot = 0, base = 0;
-      for (int c = g; c < num_chunks; c += groups) {
+      int c = g;
+      for (; c + 7 * groups < num_chunks; c += 8 * groups) {  // 8 loads in flight together
+        int v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = a.chunk_counts[static_cast<int64_t>(c + j * groups) * E + e];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          tot += v[j];
+          base += c + j * groups < chunk ? v[j] : 0;
+        }
+      }
+      for (; c < num_chunks; c += groups) {
         const int v = a.chunk_counts[static_cast<int64_t>(c) * E + e];
         tot += v;
         base += c < chunk ? v : 0;
@@ -217,14 +264,13 @@ __global__ __launch_bounds__(kChunkThreads) void route_chunk_scatter_kernel(Rout
   publish_offsets(a, s_tot, s_off, chunk == 0);
   const int64_t ntasks =
       static_cast<int64_t>(effective_tokens(a.runtime_tokens, a.host_tokens)) * a.topk;
-  const int64_t cbegin = static_cast<int64_t>(chunk) * chunk_tasks;
-  const int64_t cend = cbegin + chunk_tasks < ntasks ? cbegin + chunk_tasks : ntasks;
-  const int64_t per = ((chunk_tasks / kChunkWaves) + kWave - 1) / kWave * kWave;
-  const int64_t begin = cbegin + wave * per < cend ? cbegin + wave * per : cend;
-  const int64_t end = begin + per < cend ? begin + per : cend;
-  for (int i = tid; i < kChunkWaves * E; i += kChunkThreads) s_wbase[i / E][i % E] = 0;
+  const WaveRange wr = chunk_wave_range(ntasks, chunk, chunk_tasks, wave);
+  // the count kernel's per-wave counts of this chunk (same task split), else count again
+  const bool counted = a.wave_counts != nullptr;
+  const int32_t* wsrc = counted ? a.wave_counts + static_cast<int64_t>(chunk) * kChunkWaves * E : nullptr;
+  for (int i = tid; i < kChunkWaves * E; i += kChunkThreads) s_wbase[i / E][i % E] = counted ? wsrc[i] : 0;
   __syncthreads();
-  wave_route(a, begin, end, s_wbase[wave], [&]() {
+  wave_route(a, wr.begin, wr.end, s_wbase[wave], [&]() {
     __syncthreads();
     for (int e = tid; e < E; e += kChunkThreads) {
       int run = s_off[e] + s_cbase[e];
@@ -235,7 +281,7 @@ __global__ __launch_bounds__(kChunkThreads) void route_chunk_scatter_kernel(Rout
       }
     }
     __syncthreads();
-  });
+  }, counted);
 }
 
 }  // namespace

@@ -82,7 +82,8 @@ typedef struct mmoe_scratch_layout {
   int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R; [1] = 1: GEMM1 left
                                   the bf16 pre-activation h in y's bytes; [2] = 1: GEMM2 wrote
                                   the rows of single-slot tokens straight to y (row_dest) */
-  int64_t chunk_counts_offset; /* int32 [num_chunks, E] */
+  int64_t chunk_counts_offset; /* int32 [num_chunks, E] per-chunk counts, then
+                                  [num_chunks, 16, E] per-wave counts (routing) */
   int64_t output_index_offset; /* int32 [S_max, K]  row of (token, slot) or -1 */
   int64_t row_token_offset;    /* int32 [rows] source token of each routed row */
   int64_t row_weight_offset;   /* f32   [rows] top-k weight of each routed row */
