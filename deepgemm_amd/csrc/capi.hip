@@ -4,6 +4,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
@@ -60,6 +61,9 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
   l->row_dest_offset = take(rows * 4);
   l->sched_offset = take(2 * mmoe::kSchedInts * 4);
+  l->pipe_offset = take(mmoe::kPipeInts * 4);
+  l->pmax_offset = take(std::min<int64_t>(rows, mmoe::gemm_route_max_tasks()) *
+                        (2 * static_cast<int64_t>(intermediate) / 64) * 4);
   l->total_bytes = off;
 }
 
@@ -360,9 +364,6 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     g1.route = forward_route_args(a, l);
   }
   if (route_small_in_gemm1) g1.route = forward_route_args(a, l);
-  if (runs(MMOE_STAGE_GEMM1) &&
-      mmoe::launch_grouped_gemm(g1, max_rows, cus, s, rows_on_device, route_small_in_gemm1) != hipSuccess)
-    return MMOE_ERR_HIP;
 
   mmoe::GemmArgs g2 = g1;
   memset(&g2.sw, 0, sizeof(g2.sw));
@@ -396,21 +397,46 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     g2.direct_flag = direct_flag;
   }
 
-  // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU (after a
-  // dual GEMM1 launch it finds out on the device which GEMM1 ran)
-  const bool wide1 = mmoe::gemm_wide_selected(g1, max_rows);
-  const bool dual1 = wide1 && rows_on_device != nullptr;
-  if (runs(MMOE_STAGE_REQUANT) &&
-      mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, g1.sw, at<float>(ws, l.amax_offset),
-                           at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
-                           at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, dest,
-                           cus, s, dual1 ? rows_on_device : nullptr,
-                           mmoe::gemm_wide_min_rows(a->num_experts)) != hipSuccess)
-    return MMOE_ERR_HIP;
-
-  if (runs(MMOE_STAGE_GEMM2) &&
-      mmoe::launch_grouped_gemm(g2, max_rows, cus, s, rows_on_device) != hipSuccess)
-    return MMOE_ERR_HIP;
+  // Decode (GEMM1 routes in-kernel): GEMM1, the requant and GEMM2 in one launch, each group of
+  // rows going on to GEMM2 as soon as its GEMM1 items are done. Its counters are zeroed again by
+  // the combine, or by a fill when the call ends before the combine.
+  int32_t* pipe = nullptr;
+  if (route_in_gemm1 && runs(MMOE_STAGE_REQUANT) && runs(MMOE_STAGE_GEMM2) && !direct &&
+      mmoe::decode_pipeline_supported(g1, g2, cus)) {
+    pipe = at<int32_t>(ws, l.pipe_offset);
+    mmoe::PipeArgs p;
+    memset(&p, 0, sizeof(p));
+    p.g1 = g1;
+    p.g1.row_pmax = at<float>(ws, l.pmax_offset);
+    p.g2 = g2;
+    p.act = at<uint8_t>(ws, l.act_offset);
+    p.act_scale = at<float>(ws, l.act_scale_offset);
+    p.amax = at<float>(ws, l.amax_offset);
+    p.meta = at<int32_t>(ws, l.meta_offset);
+    p.direct_flag = direct_flag;
+    p.pipe = pipe;
+    if (mmoe::launch_decode_pipeline(p, cus, s) != hipSuccess) return MMOE_ERR_HIP;
+    if (!runs(MMOE_STAGE_COMBINE) && mmoe::launch_zero_ints(pipe, mmoe::kPipeInts, s) != hipSuccess)
+      return MMOE_ERR_HIP;
+  } else {
+    if (runs(MMOE_STAGE_GEMM1) &&
+        mmoe::launch_grouped_gemm(g1, max_rows, cus, s, rows_on_device, route_small_in_gemm1) != hipSuccess)
+      return MMOE_ERR_HIP;
+    // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU (after
+    // a dual GEMM1 launch it finds out on the device which GEMM1 ran)
+    const bool wide1 = mmoe::gemm_wide_selected(g1, max_rows);
+    const bool dual1 = wide1 && rows_on_device != nullptr;
+    if (runs(MMOE_STAGE_REQUANT) &&
+        mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, g1.sw, at<float>(ws, l.amax_offset),
+                             at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
+                             at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, dest,
+                             cus, s, dual1 ? rows_on_device : nullptr,
+                             mmoe::gemm_wide_min_rows(a->num_experts)) != hipSuccess)
+      return MMOE_ERR_HIP;
+    if (runs(MMOE_STAGE_GEMM2) &&
+        mmoe::launch_grouped_gemm(g2, max_rows, cus, s, rows_on_device) != hipSuccess)
+      return MMOE_ERR_HIP;
+  }
 
   if (runs(MMOE_STAGE_COMBINE)) {
     mmoe::CombineArgs c;
@@ -423,10 +449,14 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     c.topk = a->num_topk;
     c.hidden = a->hidden;
     c.skip_single = direct_flag;
+    c.reset = pipe;
+    c.reset_ints = pipe != nullptr ? mmoe::kPipeInts : 0;
     if (mmoe::launch_combine(c, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   }
   return MMOE_OK;
 }
+
+static_assert(MMOE_PIPE_INTS == mmoe::kPipeInts, "the header's pipeline counter count");
 
 int mmoe_forward(const mmoe_forward_args* a, void* stream) {
   return mmoe_forward_stages(a, MMOE_STAGE_ROUTE, MMOE_STAGE_COMBINE, stream);
@@ -442,8 +472,8 @@ int mmoe_forward_static(const mmoe_forward_args* args, void* stream) {
   plan_scratch(1, a.num_experts, a.num_max_tokens, a.num_topk, a.hidden, a.intermediate, &l);
   if (l.total_bytes > MMOE_STATIC_SCRATCH_BYTES) return MMOE_ERR_STATIC_SCRATCH;
   // the same launch sequence as mmoe_forward, on the static scratch of this device: nothing
-  // is allocated, and no kernel of the layer needs zeroed scratch (every table it reads was
-  // written earlier in the same call)
+  // is allocated. The array starts zero-filled, and every call leaves the only counters that
+  // must be zero when a call starts (the decode pipeline's) at zero.
   void* p = nullptr;
   const int sst = static_scratch_address(&p);
   if (sst != MMOE_OK) return sst;
@@ -459,7 +489,6 @@ int mmoe_deepep_preprocess_workspace_bytes(int recv_rows, int topk, int num_expe
       total_rows < 0)
     return MMOE_ERR_ARGUMENT;
   const int64_t tasks = static_cast<int64_t>(recv_rows) * topk;
-  const int64_t chunks = (tasks + mmoe::kRouteChunk - 1) / mmoe::kRouteChunk;
   int64_t off = 0;
   off = align_up(off + num_experts * 4, 256);            // counts
   off = align_up(off + (num_experts + 1) * 4, 256);      // offsets

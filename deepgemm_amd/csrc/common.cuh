@@ -68,10 +68,30 @@ __device__ __forceinline__ uint8_t f32_to_e4m3(float a) {
   return static_cast<uint8_t>(p & 0xff);
 }
 
+__device__ __forceinline__ float abs_max4(float m, const float4& v) {
+  return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
   return v;
+}
+
+// Max of v >= 0 over each half-wave (lanes 0-31, 32-63), valid in lanes 16-31 and 48-63 (all
+// lanes active), by DPP: quad swaps, half-row and row mirrors give every lane its 16-lane row's
+// max, then row_bcast:15 brings row 0's max into row 1 and row 2's into row 3 (other rows: 0).
+template <int kCtrl, int kRows>
+__device__ __forceinline__ float dpp_max_step(float x) {
+  return fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl, kRows, 0xf, false)));
+}
+
+__device__ __forceinline__ float half_wave_max_nonneg(float v) {
+  v = dpp_max_step<0xb1, 0xf>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_max_step<0x4e, 0xf>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_max_step<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_max_step<0x140, 0xf>(v);  // row_mirror
+  return dpp_max_step<0x142, 0xa>(v);  // row_bcast:15, rows 1 and 3
 }
 
 // Inclusive prefix sum over the 64 lanes of a wave (all lanes active), by DPP: row shifts 1, 2,

@@ -196,7 +196,7 @@ __device__ __forceinline__ void publish_tile_scales(TileTables& tt, const TileSc
 // Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
 // the output (mrows <= 64; table row trow0 + r holds row r's scales), 64-column unit `unit`
 // of the output (SwiGLU: 32 channels).
-template <bool kSwiglu, int MT>
+template <bool kSwiglu, int MT, bool kPmax = false>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[MT][2], int row0,
                                            int mrows, int unit, const TileTables& tt, int trow0) {
   const int tid = opaque_tid();
@@ -213,8 +213,10 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[
       xs[v] = tt.xs[trow0 + r];
       rw[v] = kSwiglu ? tt.rw[trow0 + r] : 0.0f;
     }
+    float pm[16];  // kPmax: |y| of the lane's channel in each of its 16 rows
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
+      pm[v] = 0.0f;
       const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
       if (r >= mrows) continue;
       if (!kSwiglu) {
@@ -222,9 +224,22 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[
         crow[0] = f32_to_bf16(acc[mt][0][v] * xs[v] * b0);
         crow[32] = f32_to_bf16(acc[mt][1][v] * xs[v] * b1);
       } else {
-        g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl] =
-            swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs[v], b0, b1, rw[v]);
+        const float yv = swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs[v], b0, b1, rw[v]);
+        g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl] = yv;
+        pm[v] = fabsf(yv);
       }
+    }
+    if constexpr (kPmax && kSwiglu) {
+      // the row maxima over the unit's 32 channels (the lanes of a half-wave); lane 16 + v of
+      // each half writes row v of its half
+#pragma unroll
+      for (int v = 0; v < 16; ++v) pm[v] = half_wave_max_nonneg(pm[v]);
+      float mv = pm[0];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) mv = (rl & 15) == v ? pm[v] : mv;
+      const int v = rl & 15;
+      const int r = mt * 32 + (v >> 2) * 8 + hk * 4 + (v & 3);
+      if (rl >= 16 && r < mrows) g.row_pmax[static_cast<int64_t>(row0 + r) * (g.n / kStreamUnit) + unit] = mv;
     }
   }
 }
@@ -258,9 +273,19 @@ __device__ __forceinline__ int swizzle_piece(int p, int r) { return (p & ~7) | (
 // next barrier. Plain loads keep the memory counter in order, so every wait the compiler places
 // for a weight step or for the staged chunk is exact; the chunk's loads are older than all
 // weight loads of chunk c and cost no wait at all by then.
-template <bool kGather, bool kSwiglu, int MT, bool kFast>
+//
+// kEarly: the weight ring's first steps go out first, then `before_a` runs (the decode
+// pipeline's wait for the item's rows), then the item's scales and A rows are loaded.
+// kAResident: before_a also leaves the item's whole A in the LDS chunk buffers (K of at most two
+// chunks), so no A rows are loaded here.
+struct NoHook {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <bool kGather, bool kSwiglu, int MT, bool kFast, bool kEarly = false, bool kAResident = false,
+          bool kPmax = false, typename Hook = NoHook>
 __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
-                            uint8_t* smem, TileTables& tt) {
+                            uint8_t* smem, TileTables& tt, const Hook& before_a = Hook{}) {
+  static_assert(!kAResident || (kEarly && kFast), "a resident A is staged by the hook");
   constexpr int D = kFast ? kStreamDepth : 1;
   constexpr int kFullChunk = kAChunk / (32 * MT);  // k-bytes per chunk
   const int kc = kFast ? kFullChunk : 128;
@@ -276,21 +301,26 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
 
   const int chunk_bytes = 32 * MT * kc;
   const uint8_t* asrc[kALoads];
+  auto a_sources = [&]() {  // (reads the row table: after before_a, which may fill it)
 #pragma unroll
-  for (int i = 0; i < kALoads; ++i) {
-    const int pos = (i * kGemmWaves + wave) * 1024 + lane * 16;
-    const int r = pos / kc;
-    const int p = swizzle_piece((pos - r * kc) >> 4, r);
-    asrc[i] = a_row_ptr<kGather>(g, rs, row0 + (r < mrows ? r : 0)) + p * 16;
-  }
+    for (int i = 0; i < kALoads; ++i) {
+      const int pos = (i * kGemmWaves + wave) * 1024 + lane * 16;
+      const int r = pos / kc;
+      const int p = swizzle_piece((pos - r * kc) >> 4, r);
+      asrc[i] = a_row_ptr<kGather>(g, rs, row0 + (r < mrows ? r : 0)) + p * 16;
+    }
+  };
+  if constexpr (!kEarly) a_sources();
   int4 astage[kALoads];
   auto load_chunk = [&](int chunk) {
+    if constexpr (kAResident) return;
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
       if (kFast || (i * kGemmWaves + wave) * 1024 < chunk_bytes)
         astage[i] = ld16(asrc[i] + static_cast<int64_t>(chunk) * kc);
   };
   auto store_chunk = [&](int chunk) {
+    if constexpr (kAResident) return;
     uint8_t* dst = smem + (chunk & 1) * kAChunk + wave * 1024 + lane * 16;
 #pragma unroll
     for (int i = 0; i < kALoads; ++i)
@@ -344,13 +374,24 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
     }
   };
 
+  if constexpr (kEarly) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      issue(d, d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    before_a();
+    if constexpr (!kAResident) a_sources();
+  }
   const TileScaleRegs tsr = load_tile_scales<kGather, kSwiglu>(g, rs, e, row0, mrows, unit);
   load_chunk(0);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (!kEarly) {
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
-    issue(d, d);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int d = 0; d < D; ++d) {
+      issue(d, d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   store_chunk(0);
   publish_tile_scales(tt, tsr, mrows);
@@ -386,7 +427,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
   }
 
   if (!active) return;
-  store_tile<kSwiglu, MT>(g, acc, row0, mrows, unit, tt, 0);
+  store_tile<kSwiglu, MT, kPmax>(g, acc, row0, mrows, unit, tt, 0);
 }
 
 // ------------------------------------------------------------------ TILE engine
@@ -918,6 +959,30 @@ __device__ void fused_rows(const RouteArgs& a, int ntasks, int e, int cnt, int o
   __syncthreads();
 }
 
+// Wave 0: the per-wave counts s_wcnt[w][e] -> per-wave bases (the wave's first rank of each
+// expert), the expert totals s_count[e] and their exclusive scan s_off[0..E] (expert offsets).
+// The LDS traffic of one wave stays in order, so a plan by the same wave can follow at once.
+__device__ void fused_scan(int E, int (*s_wcnt)[kMaxGemmExperts], int* s_count, int* s_off) {
+  const int lane = lane_id();
+  int carry = 0;
+  for (int e0 = 0; e0 < E; e0 += kWave) {
+    const int e = e0 + lane;
+    int run = 0;
+    if (e < E) {
+      for (int w = 0; w < kGemmWaves; ++w) {
+        const int c = s_wcnt[w][e];
+        s_wcnt[w][e] = run;
+        run += c;
+      }
+      s_count[e] = run;
+    }
+    const int inc = wave_inclusive_sum(run);
+    if (e < E) s_off[e] = carry + inc - run;
+    carry += __shfl(inc, kWave - 1, kWave);
+  }
+  if (lane == 0) s_off[E] = carry;
+}
+
 // ------------------------------------------------------------------ persistent dispatcher
 __device__ __forceinline__ int stream_blocks(const GemmArgs& g) {
   return (g.n / kStreamUnit + kGemmWaves - 1) / kGemmWaves;
@@ -1080,26 +1145,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
     fused_count(ra, ntasks, s_wcnt, s_ev, reinterpret_cast<float*>(smem), blockIdx.x == 0);
     __syncthreads();
     if (threadIdx.x < kWave) {
-      // wave 0: per-wave counts -> per-wave bases and expert totals, the exclusive scan of the
-      // totals (expert offsets), then the work plan; LDS traffic of one wave stays in order
-      const int lane = lane_id();
-      int carry = 0;
-      for (int e0 = 0; e0 < E; e0 += kWave) {
-        const int e = e0 + lane;
-        int run = 0;
-        if (e < E) {
-          for (int w = 0; w < kGemmWaves; ++w) {
-            const int c = s_wcnt[w][e];
-            s_wcnt[w][e] = run;
-            run += c;
-          }
-          s_count[e] = run;
-        }
-        const int inc = wave_inclusive_sum(run);
-        if (e < E) s_off[e] = carry + inc - run;
-        carry += __shfl(inc, kWave - 1, kWave);
-      }
-      if (lane == 0) s_off[E] = carry;
+      fused_scan(E, s_wcnt, s_count, s_off);
       plan_items(g, s_prefix, s_tile, s_count);
     }
     __syncthreads();
@@ -1170,6 +1216,281 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
         else if (kAnyK) stream_tile<kGather, kSwiglu, 1, false>(g, rs, e, row0, mrows, nb, smem, s_tt);
       }
     }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------ decode pipeline
+// GEMM1 (with the in-kernel routing), the requant and GEMM2 of the streaming engine in one
+// launch, so that a group of rows goes on to GEMM2 as soon as its own GEMM1 items are done,
+// instead of after the slowest XCD's last GEMM1 item, and without the requant's and GEMM2's
+// launches and prologues.
+//
+// Work: the routed rows are cut into groups (an expert's rows in chunks of kStreamRows); a group
+// has n1 GEMM1 items and n2 GEMM2 items (512-column blocks). The groups are dealt to the XCDs in
+// contiguous ranges, and the workgroups of an XCD -- found by the hardware XCD id, not by launch
+// order -- claim its queue in order: every GEMM1 item of its groups, then their GEMM2 items. A
+// claim goes out one item ahead, so its latency hides behind an item.
+//
+// Hand-off, inside the XCD, whose CUs share its L2 (the per-CU L1 is write-through): a GEMM1
+// item waits for its fp32 SwiGLU stores (vmcnt 0) and counts itself done for its group. A GEMM2
+// item issues its first weight steps, polls until its group's count is complete, invalidates
+// its CU's L1 and requantizes the group's rows from L2 straight into its LDS A buffers (the
+// requant kernel's arithmetic, so the same bits; the group's first GEMM2 item also writes act
+// and amax out). Every GEMM1 item is claimed before any GEMM2 item of its XCD, and a GEMM1 item
+// waits on nothing, so every wait ends; a wait is also bounded (kPipeSpinLimit polls), and one
+// that runs out counts in meta[3] instead of hanging. The workgroup that finishes last runs the
+// queue of any XCD that no workgroup ran (none when the launch covers the chip), alone and
+// start to end. The counters are left for the caller to zero (the combine does).
+constexpr int kPipeSpinLimit = 1 << 20;  // polls of a group count (far longer than any item)
+
+__device__ __forceinline__ int hw_xcc_id() {
+  int v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xf;
+}
+
+// This wave's outstanding memory operations (the stores a hand-off publishes) are complete.
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Later loads of this CU miss its L1 (they read the XCD's L2, where the producer's stores are).
+__device__ __forceinline__ void l1_invalidate() { asm volatile("buffer_inv sc0" ::: "memory"); }
+
+// Thread-level poll (a vector atomic load: lane-divergent code) until *c >= target.
+__device__ __forceinline__ bool wait_count(const int32_t* c, int target) {
+  for (int i = 0; i < kPipeSpinLimit; ++i) {
+    if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) return true;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return false;
+}
+
+// Wave 0: s_gprefix[0..E] = exclusive prefix of the experts' groups (chunks of kStreamRows rows).
+__device__ void plan_groups(int E, const int* s_count, int* s_gprefix) {
+  const int lane = lane_id();
+  int carry = 0;
+  for (int e0 = 0; e0 < E; e0 += kWave) {
+    const int e = e0 + lane;
+    const int n = e < E ? (s_count[e] + kStreamRows - 1) / kStreamRows : 0;
+    const int inc = wave_inclusive_sum(n);
+    if (e < E) s_gprefix[e] = carry + inc - n;
+    carry += __shfl(inc, kWave - 1, kWave);
+  }
+  if (lane == 0) s_gprefix[E] = carry;
+}
+
+// The requant of rows [row0, row0 + mrows) of GEMM1's fp32 output y into the LDS A chunk buffers
+// of a STREAM GEMM2 tile of MT 32-row tiles (stream_tile's chunk layout; K = I in one chunk for
+// MT = 1, two for MT = 2): the row's amax, inv = 448 / max(amax, 1e-4), then 16 e4m3 codes per
+// LDS piece -- the requant kernel's arithmetic, so the same bits. The amax is the max of the
+// row's 64 partial maxima that GEMM1's epilogue stored (one per 64-column block, exact), eight
+// lanes a row. Every workgroup of the group writes the rows' act_scale (the same values; the
+// tile's scale loads read them back); with write_act it also writes act and amax. The codes'
+// loads go out kStageBatch 16-byte pieces at a time.
+constexpr int kStageBatch = 4;
+
+template <int MT>
+__device__ void stage_rows_from_y(const PipeArgs& p, int row0, int mrows, bool write_act,
+                                  uint8_t* smem, float* s_inv) {
+  constexpr int kc = kAChunk / (32 * MT);
+  constexpr int kUnits = 2 * 2048 / kStreamUnit;  // partial maxima per row (I = 2048)
+  static_assert(kStreamRows == kGemmWaves * kWave / 8, "eight lanes per row cover the group");
+  const int inter = p.g1.sw.inter;
+  const int nchunks = inter / kc;
+  const int tid = opaque_tid();
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const float* y = p.g1.sw.y;
+  {
+    const int r = tid >> 3, part = (tid & 7) * (kUnits / 8);
+    const float4* src = reinterpret_cast<const float4*>(
+        p.g1.row_pmax + static_cast<int64_t>(row0 + (r < mrows ? r : 0)) * kUnits + part);
+    float4 v[kUnits / 32];
+#pragma unroll
+    for (int j = 0; j < kUnits / 32; ++j) v[j] = src[j];
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kUnits / 32; ++j) m = fmaxf(fmaxf(fmaxf(m, v[j].x), fmaxf(v[j].y, v[j].z)), v[j].w);
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
+    if ((tid & 7) == 0 && r < mrows) {
+      s_inv[r] = kE4m3Max / fmaxf(m, kAmaxFloor);
+      p.act_scale[row0 + r] = fmaxf(m, kAmaxFloor) / kE4m3Max;
+      if (write_act) p.amax[row0 + r] = m;
+    }
+  }
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    for (int i0 = 0; i0 < kALoads; i0 += kStageBatch) {
+      float4 v[kStageBatch][4];
+      int rr[kStageBatch], off[kStageBatch];
+#pragma unroll
+      for (int h = 0; h < kStageBatch; ++h) {
+        const int pos = ((i0 + h) * kGemmWaves + wave) * 1024 + lane * 16;
+        const int r = pos / kc;
+        const int piece = swizzle_piece((pos - r * kc) >> 4, r);
+        rr[h] = r;
+        off[h] = c * kc + piece * 16;
+        const float4* src = reinterpret_cast<const float4*>(
+            y + static_cast<int64_t>(row0 + (r < mrows ? r : 0)) * inter + off[h]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[h][j] = src[j];
+      }
+#pragma unroll
+      for (int h = 0; h < kStageBatch; ++h) {
+        int4 q = make_int4(0, 0, 0, 0);  // rows past mrows: never stored
+        if (rr[h] < mrows) {
+          const float inv = s_inv[rr[h]];
+          q.x = static_cast<int>(pack_e4m3x4(v[h][0].x * inv, v[h][0].y * inv, v[h][0].z * inv, v[h][0].w * inv));
+          q.y = static_cast<int>(pack_e4m3x4(v[h][1].x * inv, v[h][1].y * inv, v[h][1].z * inv, v[h][1].w * inv));
+          q.z = static_cast<int>(pack_e4m3x4(v[h][2].x * inv, v[h][2].y * inv, v[h][2].z * inv, v[h][2].w * inv));
+          q.w = static_cast<int>(pack_e4m3x4(v[h][3].x * inv, v[h][3].y * inv, v[h][3].z * inv, v[h][3].w * inv));
+          if (write_act)
+            *reinterpret_cast<int4*>(p.act + static_cast<int64_t>(row0 + rr[h]) * inter + off[h]) = q;
+        }
+        *reinterpret_cast<int4*>(smem + (c & 1) * kAChunk + wave * 1024 + lane * 16 +
+                                 (i0 + h) * kGemmWaves * 1024) = q;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ int s_gprefix[kMaxGemmExperts + 1];
+  __shared__ int s_count[kMaxGemmExperts];
+  __shared__ int s_off[kMaxGemmExperts + 1];
+  __shared__ int s_wcnt[kGemmWaves][kMaxGemmExperts];
+  __shared__ int s_tok[kRowTable];
+  __shared__ float s_rw[kRowTable];
+  __shared__ int s_task[kRowTable];
+  __shared__ uint8_t s_ev[kFusedMaxTasks];
+  __shared__ TileTables s_tt;
+  __shared__ float s_inv[kStreamRows];
+  __shared__ int s_word;  // thread 0 -> the workgroup
+  const GemmArgs& g1 = p.g1;
+  const GemmArgs& g2 = p.g2;
+  const RouteArgs& ra = g1.route;
+  const int E = g1.num_experts;
+  int32_t* const claims = p.pipe;                                                          // [kPipeXcds]
+  unsigned long long* const finish = reinterpret_cast<unsigned long long*>(p.pipe + kPipeXcds);
+  int32_t* const done1 = p.pipe + kPipeHeader;                                             // [groups]
+  const int hw = hw_xcc_id();
+  const int home = hw & (kPipeXcds - 1);
+  int x = home;
+  // thread 0: this XCD's presence (the finish word's high half; complete before the workgroup
+  // counts itself finished) and the first claim; both latencies hide behind the routing
+  int pending = 0;
+  unsigned long long seen = 0;
+  if (threadIdx.x == 0) {
+    seen = atomicOr(finish, 1ull << (32 + home));
+    pending = atomicAdd(&claims[x], 1);
+  }
+  const int ntasks = effective_tokens(ra.runtime_tokens, ra.host_tokens) * ra.topk;
+  {
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    for (int e = lane_id(); e < E; e += kWave) s_wcnt[wave][e] = 0;
+  }
+  fused_count(ra, ntasks, s_wcnt, s_ev, reinterpret_cast<float*>(smem), blockIdx.x == 0);
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    fused_scan(E, s_wcnt, s_count, s_off);
+    plan_groups(E, s_count, s_gprefix);
+  }
+  __syncthreads();
+  if (blockIdx.x == 0) {  // the routing outputs that the later stages read
+    for (int e = threadIdx.x; e <= E; e += kGemmThreads) ra.offsets[e] = s_off[e];
+    for (int e = threadIdx.x; e < E; e += kGemmThreads) {
+      ra.counts[e] = s_count[e];
+      if (ra.stats != nullptr) ra.stats[e] += s_count[e];
+    }
+    if (threadIdx.x == 0) {
+      ra.meta[0] = s_off[E] < ra.row_cap ? s_off[E] : static_cast<int>(ra.row_cap);
+      p.meta[1] = 0;  // the requant read GEMM1's y
+      p.meta[3] = 0;  // bounded waits that ran out (none can have by now)
+      if (p.direct_flag != nullptr) *p.direct_flag = 0;
+      if (hw >= kPipeXcds) atomicAdd(&p.meta[3], 1);  // an XCD id this launch does not expect
+    }
+  }
+  const int G = s_gprefix[E];
+  if (G > kMaxPipeGroups) {  // more groups than counters (the host's task bound rules it out)
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&p.meta[3], 1);
+    return;
+  }
+  const int n1 = stream_blocks(g1), n2 = stream_blocks(g2);
+  const float* task_w = reinterpret_cast<const float*>(smem);  // valid until the first item's loads
+  bool first_item = true;
+  int present = -1;  // the last workgroup: XCDs that had workgroups (bit mask)
+  int orphan = -1;   // the last workgroup: the XCD queue it runs
+  if (threadIdx.x == 0) asm volatile("" ::"v"(seen));  // the presence bit is set from here on
+  for (;;) {
+    if (threadIdx.x == 0) s_word = pending;
+    __syncthreads();
+    const int t = s_word;
+    __syncthreads();
+    const int gb = static_cast<int>(static_cast<int64_t>(G) * x / kPipeXcds);
+    const int ng = static_cast<int>(static_cast<int64_t>(G) * (x + 1) / kPipeXcds) - gb;
+    if (t >= (n1 + n2) * ng) {
+      if (present < 0) {
+        // count this workgroup finished; the last one learns which XCDs had workgroups
+        if (threadIdx.x == 0) {
+          const unsigned long long old = atomicAdd(finish, 1ull);
+          const bool is_last = static_cast<unsigned>(old & 0xffffffffull) == gridDim.x - 1;
+          s_word = is_last ? static_cast<int>((old >> 32) | (1ull << home)) : -1;
+        }
+        __syncthreads();
+        present = s_word;
+        __syncthreads();
+        if (present < 0) break;
+      }
+      // every other workgroup has finished: the queues of XCDs without workgroups, whole
+      do ++orphan; while (orphan < kPipeXcds && ((present >> orphan) & 1));
+      if (orphan >= kPipeXcds) break;
+      x = orphan;
+      if (threadIdx.x == 0) pending = atomicAdd(&claims[x], 1);
+      continue;
+    }
+    if (threadIdx.x == 0) pending = atomicAdd(&claims[x], 1);  // the next claim, one item ahead
+    const bool gemm1 = t < n1 * ng;
+    const int local = gemm1 ? t : t - n1 * ng;
+    const int per = gemm1 ? n1 : n2;
+    const int grp = gb + local / per;
+    const int nb = local - (local / per) * per;
+    const int e = expert_of_item(s_gprefix, E, grp);
+    const int r0 = (grp - s_gprefix[e]) * kStreamRows;
+    const int cnt = s_count[e];
+    const int off_e = s_off[e];
+    const int mrows = min(kStreamRows, cnt - r0);
+    const int row0 = off_e + r0;
+    if (gemm1) {
+      // the weights go out first; then the item's rows are ranked into the LDS row table
+      const float* item_w = first_item ? task_w : nullptr;
+      const auto rank_rows = [&]() {
+        fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, item_w, r0, nb == 0 ? r0 : 0,
+                   nb == 0 ? r0 + kStreamRows : 0, 0, 0, s_task, s_tok, s_rw);
+      };
+      const RowSrc rs{s_tok, s_rw, row0};
+      if (mrows > 32) stream_tile<true, true, 2, true, true, false, true>(g1, rs, e, row0, mrows, nb, smem, s_tt, rank_rows);
+      else stream_tile<true, true, 1, true, true, false, true>(g1, rs, e, row0, mrows, nb, smem, s_tt, rank_rows);
+      vm_drain();  // this wave's y stores are in L2
+      __syncthreads();
+      if (threadIdx.x == 0) atomicAdd(&done1[grp], 1);
+    } else {
+      // the weights go out first; then the group's rows, requantized from y into LDS
+      const auto stage_rows = [&]() {
+        if (threadIdx.x == 0 && !wait_count(&done1[grp], n1)) atomicAdd(&p.meta[3], 1);
+        __syncthreads();
+        l1_invalidate();
+        if (mrows > 32) stage_rows_from_y<2>(p, row0, mrows, nb == 0, smem, s_inv);
+        else stage_rows_from_y<1>(p, row0, mrows, nb == 0, smem, s_inv);
+        vm_drain();  // act_scale is read back by the tile's scale loads
+        __syncthreads();
+        l1_invalidate();  // (a line of act_scale may hold another group's rows, read earlier)
+      };
+      const RowSrc rs{nullptr, nullptr, 0};
+      if (mrows > 32) stream_tile<false, false, 2, true, true, true>(g2, rs, e, row0, mrows, nb, smem, s_tt, stage_rows);
+      else stream_tile<false, false, 1, true, true, true>(g2, rs, e, row0, mrows, nb, smem, s_tt, stage_rows);
+    }
+    first_item = false;
     __syncthreads();
   }
 }
@@ -1351,6 +1672,30 @@ constexpr int kWideBM2 = 256;
 
 int gemm_wide_min_rows(int num_experts) {
   return std::max(kFusedMaxTasks + 1, kWideMinRowsPerExpert * num_experts);
+}
+
+// The decode pipeline needs the streaming engine's full-chunk shapes for both GEMMs (GEMM2's
+// K = I in at most two chunks, staged whole by the requant), GEMM1's in-kernel routing, and
+// the whole MI355X (8 XCDs of 32 CUs: its queues are the hardware XCD ids).
+bool decode_pipeline_supported(const GemmArgs& g1, const GemmArgs& g2, int num_cus) {
+  return num_cus == kPipeXcds * 32 && g1.engine != GemmEngine::kTile && g2.engine != GemmEngine::kTile &&
+         g1.route_in_kernel == 1 && g1.sw.enabled && g1.num_experts <= kFusedMaxExperts &&
+         g1.k % (kAChunk / 32) == 0 && g2.k == kAChunk / 32 && g1.n == 2 * g1.sw.inter &&
+         g2.k == g1.sw.inter && g1.n % (kStreamUnit * kGemmWaves) == 0 &&
+         g2.n % (kStreamUnit * kGemmWaves) == 0 && g1.row_token != nullptr && g2.row_token == nullptr &&
+         g1.dual_rows == nullptr && g2.dual_rows == nullptr && g2.y_direct == nullptr;
+}
+
+hipError_t launch_decode_pipeline(const PipeArgs& p, int num_cus, hipStream_t stream) {
+  if (!decode_pipeline_supported(p.g1, p.g2, num_cus) || p.pipe == nullptr || p.g1.row_pmax == nullptr ||
+      p.act != p.g2.a ||
+      p.act_scale != p.g2.a_scale || p.g2.lda != p.g1.sw.inter)
+    return hipErrorInvalidValue;
+  const hipError_t err = ensure_dynamic_lds<&decode_pipeline_kernel>(kSmemBytes);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(decode_pipeline_kernel, dim3(static_cast<unsigned>(num_cus)), dim3(kGemmThreads),
+                     kSmemBytes, stream, p);
+  return hipGetLastError();
 }
 
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream,

@@ -95,6 +95,9 @@ struct GemmArgs {
   // meta[0]) select it -- WIDE at dual_min_rows or more. Null: the launch always runs.
   const int32_t* dual_rows;
   int dual_min_rows;
+  // Decode pipeline GEMM1: per row, the max |SwiGLU output| of each 64-column unit (float
+  // [rows, n / 64]), which the pipeline's requant takes its row maxima from. Null: not written.
+  float* row_pmax;
 };
 constexpr int kSchedInts = 16;
 
@@ -159,8 +162,33 @@ struct CombineArgs {
   int host_tokens;
   int topk;
   int hidden;
+  int32_t* reset;                  // null, or reset_ints ints set to zero (the decode pipeline's
+  int reset_ints;                  // counters, which the next call needs at zero)
 };
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream);
+hipError_t launch_zero_ints(int32_t* p, int n, hipStream_t stream);
+
+// Decode pipeline (gemm.hip): GEMM1 with the in-kernel routing, the requant and GEMM2 of the
+// streaming engine in one launch, each group of rows handed from GEMM1 to GEMM2 inside its XCD.
+// pipe: kPipeInts counters, zero when the launch starts (the combine zeroes them again,
+// CombineArgs::reset): [0..7] per-XCD claim counters, [8..9] the finish word (u64: finished
+// workgroups | XCDs that had workgroups << 32), [kPipeHeader..] GEMM1 items done per group.
+constexpr int kPipeXcds = 8;
+constexpr int kPipeHeader = 16;
+constexpr int kMaxPipeGroups = 512;  // groups of <= 64 rows: S*K <= 8192 rows over <= 255 experts
+constexpr int kPipeInts = kPipeHeader + kMaxPipeGroups;
+struct PipeArgs {
+  GemmArgs g1;           // GEMM1: route_in_kernel 1, SwiGLU epilogue into the fp32 y
+  GemmArgs g2;           // GEMM2: a = act, a_scale = act_scale
+  uint8_t* act;          // e4m3 [rows, I] (written by the first GEMM2 item of each group)
+  float* act_scale;      // [rows]
+  float* amax;           // [rows] (with act)
+  int32_t* meta;         // [1] = 0 (the requant read y); [3] = bounded waits that ran out
+  int32_t* direct_flag;  // set to 0 (no direct rows), or null
+  int32_t* pipe;
+};
+bool decode_pipeline_supported(const GemmArgs& g1, const GemmArgs& g2, int num_cus);
+hipError_t launch_decode_pipeline(const PipeArgs& p, int num_cus, hipStream_t stream);
 
 // For every task (token t, slot s) with row = output_index[t*K+s] >= 0:
 // grouped_x[row] = x[t], grouped_scale[row] = x_sf[t].

@@ -280,7 +280,9 @@ class SymmBuffer:
         row_token, row_weight, m_indices, act_scale, amax (max |y| per row), y (SwiGLU x
         weight, f32), act (requantised y), part (GEMM2 rows), row_dest (the token whose y
         row GEMM2 wrote directly for a row, else -1; built in calls with the WIDE GEMMs, where
-        those rows' part is not written; meta[2] == 1 then). When meta[1] == 1 the GEMM1 of
+        those rows' part is not written; meta[2] == 1 then), sched and pipe (the GEMMs' work
+        counters, zero between calls), pmax (per row, max |y| of each 64-column block of GEMM1's
+        output; written by the one-launch decode pipeline only). When meta[1] == 1 the GEMM1 of
         the call left the bf16 pre-activation instead of y, in the same bytes: view it as h
         ([rows, 2I], gate channels then up channels)."""
         l = self.scratch_layout
@@ -302,6 +304,9 @@ class SymmBuffer:
             "part": (l.part_offset, torch.bfloat16, (rows, self.hidden)),
             "row_dest": (l.row_dest_offset, torch.int32, (rows,)),
             "sched": (l.sched_offset, torch.int32, (2, 16)),
+            "pipe": (l.pipe_offset, torch.int32, (_capi.MMOE_PIPE_INTS,)),
+            "pmax": (l.pmax_offset, torch.float32,
+                     (min(rows, 8192), 2 * self.intermediate_hidden // 64)),
         }
         off, dtype, shape = spec[name]
         n = 1

@@ -47,7 +47,8 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_struct_layouts_match_c_compiler(tmp_path):
-    """sizeof/offsetof of every header struct as gcc lays it out == the ctypes mirrors."""
+    """sizeof/offsetof of every header struct as gcc lays it out == the ctypes mirrors (and the
+    header's counter count == the binding's)."""
     structs = {"mmoe_forward_args": _capi.ForwardArgs, "mmoe_symm_layout": _capi.SymmLayout,
                "mmoe_scratch_layout": _capi.ScratchLayout}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "megamoe_hip.h"',
@@ -56,6 +57,7 @@ def test_struct_layouts_match_c_compiler(tmp_path):
         lines.append(f'printf("{cname} %zu\\n", sizeof({cname}));')
         for fname, _ in py._fields_:
             lines.append(f'printf("{cname}.{fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append('printf("MMOE_PIPE_INTS %d\\n", MMOE_PIPE_INTS);')
     lines.append("return 0; }")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -66,6 +68,7 @@ def test_struct_layouts_match_c_compiler(tmp_path):
     out = dict(line.rsplit(" ", 1) for line in
                subprocess.run([str(exe)], capture_output=True, text=True,
                               check=True).stdout.split("\n") if line)
+    assert int(out["MMOE_PIPE_INTS"]) == _capi.MMOE_PIPE_INTS
     for cname, py in structs.items():
         assert int(out[cname]) == ctypes.sizeof(py), cname
         for fname, _ in py._fields_:

@@ -117,6 +117,7 @@ def test_routing_bit_exact(mm, cuda, name):
 # ------------------------------------------------------------------ the layer
 def _stage_checks(buf, tr, s, clamp=None):
     r = tr.routing.num_rows
+    assert buf.scratch_view("meta")[3].item() == 0, "decode pipeline: a bounded wait ran out"
     from_h = buf.scratch_view("meta")[1].item() == 1
     if from_h:
         # the 4-wave GEMM1 leaves the bf16 pre-activation h; requant applies the SwiGLU with
@@ -508,6 +509,37 @@ def test_wide_claim_counters_return_to_zero(mm, cuda):
     mm.LayerCall(torch.empty_like(y1), l1, l2, buf).run(3, 3)  # GEMM2 alone
     torch.cuda.synchronize()
     assert torch.all(buf.scratch_view("sched").cpu() == 0)
+    y2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+def test_decode_pipeline_counters_and_row_maxima(mm, cuda, full_weights):
+    """The one-launch decode pipeline (GEMM1 + requant + GEMM2 of the 8-wave kernel on the
+    256-CU chip, S*K <= 8192): GEMM1's per-block row maxima are exactly the blocks' max |y| and
+    reduce to the requant's row amax; its hand-off counters read zero after a whole call and
+    after a call that stops before the combine; calls on the same scratch are bitwise equal."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the decode pipeline runs on the whole 256-CU MI355X only")
+    l1, l2, l1c, l2c, unpacked = full_weights
+    s = 512
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=77)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
+    log("decode pipeline counters and row maxima")
+    y1 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2).clone()
+    torch.cuda.synchronize()
+    assert buf.scratch_view("meta")[3].item() == 0
+    assert torch.all(buf.scratch_view("pipe").cpu() == 0)
+    r = int(buf.scratch_view("meta")[0].item())
+    y = buf.scratch_view("y")[:r].cpu()
+    pmax = buf.scratch_view("pmax")[:r].cpu()
+    assert torch.equal(pmax, y.view(r, 64, 32).abs().amax(dim=2)), "per-block row maxima"
+    assert torch.equal(buf.scratch_view("amax")[:r].cpu(), pmax.amax(dim=1)), "row amax"
+    buf.scratch_view("pmax").fill_(-1.0)
+    mm.LayerCall(torch.empty_like(y1), l1, l2, buf).run(0, 3)  # stops before the combine
+    torch.cuda.synchronize()
+    assert bool((buf.scratch_view("pmax")[:r] >= 0).all()), "the pipeline ran"
+    assert torch.all(buf.scratch_view("pipe").cpu() == 0)
     y2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
     torch.cuda.synchronize()
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
