@@ -65,13 +65,15 @@ def algorithmic_bytes(rows: int, touched: int) -> dict:
              + rows * (i + 4) * 2 + rows * h * 2)
     gemm1 = touched * 2 * i * h + touched * 2 * i * 4 + rows * (h + 4) + rows * 2 * i * 2
     gemm2 = touched * h * i + touched * h * 4 + rows * (i + 4) + rows * h * 2
-    return dict(layer=layer, gemm1=gemm1, gemm2=gemm2)
+    # the decode pipeline runs both GEMMs (and the requant between them) in one launch
+    return dict(layer=layer, gemm1=gemm1, gemm2=gemm2, pipeline=gemm1 + gemm2)
 
 
 # kernel names as rocprofv3 reports them: the 8-wave persistent kernel (decode-sized configs)
 # or the 4-wave WIDE kernel (many rows per expert)
 PROFILE_KERNELS = {"gemm1": ("grouped_gemm_kernel<true, true, false>", "wide_gemm_kernel<true, true, 256>"),
-                   "gemm2": ("grouped_gemm_kernel<false, false, false>", "wide_gemm_kernel<false, false, 256>")}
+                   "gemm2": ("grouped_gemm_kernel<false, false, false>", "wide_gemm_kernel<false, false, 256>"),
+                   "pipeline": ("decode_pipeline_kernel",)}
 
 
 def profiled_traffic(config_id: str, kernel: str):
@@ -213,11 +215,15 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     def layer():
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf)
 
+    # the one-launch decode pipeline (routing, GEMM1, requant and GEMM2) is the only kernel that
+    # writes the per-block row maxima: whether it ran is read back from them
+    buf.scratch_view("pmax").fill_(-1.0)
     for _ in range(max(1, args.warmup)):
         layer()
     torch.cuda.synchronize()
     counts = buf.scratch_view("counts").cpu()
     rows = int(counts.sum())
+    pipeline = rows > 0 and bool((buf.scratch_view("pmax")[:rows] >= 0).all())
     touched = int((counts > 0).sum())
     log(f"  routed rows R={rows}, touched experts={touched}, largest expert={int(counts.max())}")
 
@@ -240,10 +246,15 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     if not args.no_stage_timing:
         # The stages as the layer runs them: when GEMM1 routes in-kernel (small task counts)
         # routing and GEMM1 are one launch and are timed together.
+        # With the decode pipeline, routing through GEMM2 is one launch.
         call = mm.LayerCall(y, l1, l2, buf)
         fused_route = s * TOPK <= ROUTE_IN_GEMM1_MAX_TASKS
-        groups = ([("gemm1", 0, 1)] if fused_route else [("route", 0, 0), ("gemm1", 1, 1)])
-        groups += [("requant", 2, 2), ("gemm2", 3, 3), ("combine", 4, 4)]
+        if pipeline:
+            groups = [("pipeline", 0, 3)]
+        else:
+            groups = ([("gemm1", 0, 1)] if fused_route else [("route", 0, 0), ("gemm1", 1, 1)])
+            groups += [("requant", 2, 2), ("gemm2", 3, 3)]
+        groups += [("combine", 4, 4)]
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(groups) + 1)]
               for _ in range(args.steps)]
         for i in range(args.steps):
@@ -264,7 +275,7 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     bound = "hbm" if flops / max(nbytes["layer"], 1) < FP8_PEAK_FLOPS / HBM_PEAK_BPS else "mfma"
     roofline = None
     if stage_ms is not None:
-        dom = max(("gemm1", "gemm2"), key=lambda k: stage_ms[k])
+        dom = "pipeline" if pipeline else max(("gemm1", "gemm2"), key=lambda k: stage_ms[k])
         dom_s = stage_ms[dom] * 1e-3
         prof = profiled_traffic(name, dom)
         if bound == "hbm":
@@ -276,7 +287,7 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
                             algorithmic_bytes=nbytes[dom], avg_us=round(stage_ms[dom] * 1e3, 2),
                             traffic_source=prof[1] if prof else None)
         else:
-            kflops = 2.0 * rows * HIDDEN * (2 * INTER if dom == "gemm1" else INTER)
+            kflops = 2.0 * rows * HIDDEN * {"gemm1": 2 * INTER, "gemm2": INTER, "pipeline": 3 * INTER}[dom]
             achieved = kflops / dom_s / 1e12
             roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 1),
                             peak=FP8_PEAK_FLOPS / 1e12, unit="TFLOP/s",

@@ -398,12 +398,10 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   }
 
   // Decode (GEMM1 routes in-kernel): GEMM1, the requant and GEMM2 in one launch, each group of
-  // rows going on to GEMM2 as soon as its GEMM1 items are done. Its counters are zeroed again by
-  // the combine, or by a fill when the call ends before the combine.
-  int32_t* pipe = nullptr;
+  // rows going on to GEMM2 as soon as its GEMM1 items are done. Its last workgroup sets its
+  // counters back to zero.
   if (route_in_gemm1 && runs(MMOE_STAGE_REQUANT) && runs(MMOE_STAGE_GEMM2) && !direct &&
       mmoe::decode_pipeline_supported(g1, g2, cus)) {
-    pipe = at<int32_t>(ws, l.pipe_offset);
     mmoe::PipeArgs p;
     memset(&p, 0, sizeof(p));
     p.g1 = g1;
@@ -414,10 +412,8 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     p.amax = at<float>(ws, l.amax_offset);
     p.meta = at<int32_t>(ws, l.meta_offset);
     p.direct_flag = direct_flag;
-    p.pipe = pipe;
+    p.pipe = at<int32_t>(ws, l.pipe_offset);
     if (mmoe::launch_decode_pipeline(p, cus, s) != hipSuccess) return MMOE_ERR_HIP;
-    if (!runs(MMOE_STAGE_COMBINE) && mmoe::launch_zero_ints(pipe, mmoe::kPipeInts, s) != hipSuccess)
-      return MMOE_ERR_HIP;
   } else {
     if (runs(MMOE_STAGE_GEMM1) &&
         mmoe::launch_grouped_gemm(g1, max_rows, cus, s, rows_on_device, route_small_in_gemm1) != hipSuccess)
@@ -449,8 +445,6 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     c.topk = a->num_topk;
     c.hidden = a->hidden;
     c.skip_single = direct_flag;
-    c.reset = pipe;
-    c.reset_ints = pipe != nullptr ? mmoe::kPipeInts : 0;
     if (mmoe::launch_combine(c, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   }
   return MMOE_OK;

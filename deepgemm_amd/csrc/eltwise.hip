@@ -146,8 +146,6 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
 // V = 8 (whole 4096-column rows) for many tokens; V = 2 spreads few tokens over more waves.
 template <int V>
 __global__ __launch_bounds__(kEltThreads) void combine_kernel(CombineArgs c) {
-  if (blockIdx.x == 0 && c.reset != nullptr)
-    for (int i = threadIdx.x; i < c.reset_ints; i += kEltThreads) c.reset[i] = 0;
   const int lane = lane_id();
   const int tokens = effective_tokens(c.runtime_tokens, c.host_tokens);
   const int nvec = c.hidden >> 3;
@@ -224,8 +222,6 @@ __global__ __launch_bounds__(kEltThreads) void combine_kernel(CombineArgs c) {
 
 // Scalar tail of the combine for hidden % 8 != 0 (kept simple; the layer uses H % 128 == 0).
 __global__ __launch_bounds__(kEltThreads) void combine_scalar_kernel(CombineArgs c) {
-  if (blockIdx.x == 0 && c.reset != nullptr)
-    for (int i = threadIdx.x; i < c.reset_ints; i += kEltThreads) c.reset[i] = 0;
   const int tokens = effective_tokens(c.runtime_tokens, c.host_tokens);
   for (int t = blockIdx.x; t < tokens; t += gridDim.x) {
     for (int h = threadIdx.x; h < c.hidden; h += kEltThreads) {
@@ -355,7 +351,7 @@ hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw
 }
 
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream) {
-  if (c.host_tokens <= 0) return c.reset != nullptr ? launch_zero_ints(c.reset, c.reset_ints, stream) : hipSuccess;
+  if (c.host_tokens <= 0) return hipSuccess;
   if (c.topk > 16) return hipErrorInvalidValue;
   if ((c.hidden & 7) == 0) {
     // a wave per item, up to 8 four-wave workgroups a CU in flight; whole rows once there are
@@ -402,19 +398,6 @@ hipError_t launch_marlin_pack(uint8_t* out, const uint8_t* in, int64_t groups, i
   if (total <= 0) return hipSuccess;
   hipLaunchKernelGGL(marlin_pack_kernel, dim3(grid_for(total, kEltThreads, 65536)),
                      dim3(kEltThreads), 0, stream, out, in, groups, rows, k);
-  return hipGetLastError();
-}
-
-namespace {
-__global__ __launch_bounds__(kEltThreads) void zero_ints_kernel(int32_t* p, int n) {
-  for (int i = blockIdx.x * kEltThreads + threadIdx.x; i < n; i += gridDim.x * kEltThreads) p[i] = 0;
-}
-}  // namespace
-
-hipError_t launch_zero_ints(int32_t* p, int n, hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_ints_kernel, dim3(grid_for(n, kEltThreads, 1024)), dim3(kEltThreads), 0,
-                     stream, p, n);
   return hipGetLastError();
 }
 

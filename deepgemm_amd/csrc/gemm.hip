@@ -1241,7 +1241,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 // waits on nothing, so every wait ends; a wait is also bounded (kPipeSpinLimit polls), and one
 // that runs out counts in meta[3] instead of hanging. The workgroup that finishes last runs the
 // queue of any XCD that no workgroup ran (none when the launch covers the chip), alone and
-// start to end. The counters are left for the caller to zero (the combine does).
+// start to end, and then sets the counters back to zero.
 constexpr int kPipeSpinLimit = 1 << 20;  // polls of a group count (far longer than any item)
 
 __device__ __forceinline__ int hw_xcc_id() {
@@ -1411,11 +1411,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
       if (hw >= kPipeXcds) atomicAdd(&p.meta[3], 1);  // an XCD id this launch does not expect
     }
   }
-  const int G = s_gprefix[E];
-  if (G > kMaxPipeGroups) {  // more groups than counters (the host's task bound rules it out)
-    if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&p.meta[3], 1);
-    return;
-  }
+  // more groups than counters (the host's task bound rules it out): flagged, and no items
+  const bool too_many = s_gprefix[E] > kMaxPipeGroups;
+  if (too_many && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&p.meta[3], 1);
+  const int G = too_many ? 0 : s_gprefix[E];
   const int n1 = stream_blocks(g1), n2 = stream_blocks(g2);
   const float* task_w = reinterpret_cast<const float*>(smem);  // valid until the first item's loads
   bool first_item = true;
@@ -1493,6 +1492,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
     first_item = false;
     __syncthreads();
   }
+  // the last workgroup, alone now (every other one has counted itself finished after its last
+  // claim was answered and its hand-off counts were done): the counters back to zero for the
+  // next launch
+  if (present >= 0)
+    for (int i = threadIdx.x; i < kPipeInts; i += kGemmThreads) p.pipe[i] = 0;
 }
 
 // Persistent dispatcher of the WIDE engine: every expert's rows as BM x 256 tiles, items dealt

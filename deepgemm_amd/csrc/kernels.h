@@ -162,17 +162,14 @@ struct CombineArgs {
   int host_tokens;
   int topk;
   int hidden;
-  int32_t* reset;                  // null, or reset_ints ints set to zero (the decode pipeline's
-  int reset_ints;                  // counters, which the next call needs at zero)
 };
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream);
-hipError_t launch_zero_ints(int32_t* p, int n, hipStream_t stream);
 
 // Decode pipeline (gemm.hip): GEMM1 with the in-kernel routing, the requant and GEMM2 of the
 // streaming engine in one launch, each group of rows handed from GEMM1 to GEMM2 inside its XCD.
-// pipe: kPipeInts counters, zero when the launch starts (the combine zeroes them again,
-// CombineArgs::reset): [0..7] per-XCD claim counters, [8..9] the finish word (u64: finished
-// workgroups | XCDs that had workgroups << 32), [kPipeHeader..] GEMM1 items done per group.
+// pipe: kPipeInts counters, zero when the launch starts (its last workgroup zeroes them
+// again): [0..7] per-XCD claim counters, [8..9] the finish word (u64: finished workgroups |
+// XCDs that had workgroups << 32), [kPipeHeader..] GEMM1 items done per group.
 constexpr int kPipeXcds = 8;
 constexpr int kPipeHeader = 16;
 constexpr int kMaxPipeGroups = 512;  // groups of <= 64 rows: S*K <= 8192 rows over <= 255 experts
