@@ -545,6 +545,35 @@ def test_decode_pipeline_counters_and_row_maxima(mm, cuda, full_weights):
     assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
 
 
+@pytest.mark.parametrize("e,s,g", [(96, 512, 256), (160, 1024, 256)])
+def test_decode_pipeline_many_experts(mm, cuda, e, s, g):
+    """The one-launch decode pipeline over more than 64 local experts (its group plan scans the
+    experts in 64-wide chunks) with several groups a workgroup: every stage against the oracle,
+    the combine bitwise, counters back at zero."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the decode pipeline runs on the whole 256-CU MI355X only")
+    log(f"decode pipeline E={e} S={s}")
+    l1, l2 = make_weights_gpu(e, 4096, 2048, seed=500 + e, mm=mm)
+    torch.cuda.synchronize()
+    l1c, l2c = cpu_weights(l1, l2)
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, e, 6, seed=600 + e, global_experts=g)
+    buf = mm.get_symm_buffer_for_mega_moe(None, e, s, 6, 4096, 2048)
+    buf.scratch_view("pmax").fill_(-1.0)
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c)
+    r = tr.routing.num_rows
+    assert (tr.routing.counts > 0).sum() > 64 and tr.routing.counts.max() <= 64
+    assert bool((buf.scratch_view("pmax")[:r] >= 0).all()), "the pipeline ran"
+    assert torch.all(buf.scratch_view("pipe").cpu() == 0)
+    _stage_checks(buf, tr, s)
+    _combine_bitwise(mm, buf, y, l1, l2, s, None)
+    d = O.calc_diff(y.cpu(), tr.y)
+    log(f"  calc_diff={d:.3e}")
+    assert d <= CALC_DIFF_BAR
+    del l1, l2
+
+
 def test_layer_no_routed_rows(mm, cuda):
     """Every slot invalid -> y == 0 exactly (no partial contributes)."""
     s, e, hdim, inter = 10, 4, 256, 128
