@@ -138,8 +138,8 @@ __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
 
 // ---------------------------------------------------------------- combine
 // One wave per (token, piece of V*64 16-byte column groups), grid-stride over those items; the
-// next item's slot rows are loaded while the current one is summed, so an item costs one round
-// trip per routed slot. Lanes 0..K-1 hold the token's slot rows; every lane owns the 16-byte
+// next item's slot rows are loaded while the current one is summed, and the partial rows of up
+// to 4 (V = 2) or 2 (V = 8) slots are loaded together. Lanes 0..K-1 hold the token's slot rows; every lane owns the 16-byte
 // groups lane + 64j of the piece. Slots are summed in ascending order into fp32 accumulators
 // that start at +0 (the reference's order); a token without routed slots gets zeros, and with
 // skip_single a token with exactly one routed slot is left alone (GEMM2 wrote that row to y).
@@ -182,27 +182,41 @@ __global__ __launch_bounds__(kEltThreads) void combine_kernel(CombineArgs c) {
       for (int j = 0; j < V; ++j)
 #pragma unroll
         for (int q = 0; q < 8; ++q) sum[j][q] = 0.0f;
-      for (uint64_t m = routed; m != 0; m &= m - 1) {
-        const int s = __ffsll(static_cast<unsigned long long>(m)) - 1;
-        const int r = __shfl(row, s, kWave);
-        const float ws = __shfl(w, s, kWave);
-        const uint4* prow = reinterpret_cast<const uint4*>(c.part + static_cast<int64_t>(r) * c.hidden);
-        uint4 p[V];
+      // the routed slots in ascending order, kSlots at a time: their rows' loads go out together
+      // (one round trip per batch instead of one per slot), the sums stay in slot order
+      constexpr int kSlots = V <= 2 ? 4 : 2;
+      for (uint64_t m = routed; m != 0;) {
+        uint4 p[kSlots][V];
+        float ws[kSlots];
+        bool has[kSlots];
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
-          const int v = v0 + j * kWave + lane;
-          p[j] = v < nvec ? ld_nt(prow + v) : make_uint4(0, 0, 0, 0);
+        for (int b = 0; b < kSlots; ++b) {
+          has[b] = m != 0;  // wave-uniform (a ballot)
+          const int s = has[b] ? __ffsll(static_cast<unsigned long long>(m)) - 1 : 0;
+          m &= m - 1;
+          const int r = __shfl(row, s, kWave);
+          ws[b] = __shfl(w, s, kWave);
+          const uint4* prow = reinterpret_cast<const uint4*>(c.part + static_cast<int64_t>(r) * c.hidden);
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            const int v = v0 + j * kWave + lane;
+            p[b][j] = has[b] && v < nvec ? ld_nt(prow + v) : make_uint4(0, 0, 0, 0);
+          }
         }
 #pragma unroll
-        for (int j = 0; j < V; ++j) {
-          const uint32_t words[4] = {p[j].x, p[j].y, p[j].z, p[j].w};
+        for (int b = 0; b < kSlots; ++b) {
+          if (!has[b]) break;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float lo = bf16_to_f32(words[q] & 0xffff);
-            float hi = bf16_to_f32(words[q] >> 16);
-            if (c.apply_weights) { lo *= ws; hi *= ws; }
-            sum[j][2 * q] += lo;
-            sum[j][2 * q + 1] += hi;
+          for (int j = 0; j < V; ++j) {
+            const uint32_t words[4] = {p[b][j].x, p[b][j].y, p[b][j].z, p[b][j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float lo = bf16_to_f32(words[q] & 0xffff);
+              float hi = bf16_to_f32(words[q] >> 16);
+              if (c.apply_weights) { lo *= ws[b]; hi *= ws[b]; }
+              sum[j][2 * q] += lo;
+              sum[j][2 * q + 1] += hi;
+            }
           }
         }
       }
