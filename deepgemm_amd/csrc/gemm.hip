@@ -1371,20 +1371,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
   const GemmArgs& g2 = p.g2;
   const RouteArgs& ra = g1.route;
   const int E = g1.num_experts;
-  int32_t* const claims = p.pipe;                                                          // [kPipeXcds]
-  unsigned long long* const finish = reinterpret_cast<unsigned long long*>(p.pipe + kPipeXcds);
-  int32_t* const done1 = p.pipe + kPipeHeader;                                             // [groups]
+  int32_t* const claims = p.pipe;  // XCD x's counter at claims[x * kPipeLine]
+  int32_t* const finish = p.pipe + kPipeXcds * kPipeLine;
+  int32_t* const done1 = p.pipe + kPipeHeader;  // [groups]
   const int hw = hw_xcc_id();
   const int home = hw & (kPipeXcds - 1);
   int x = home;
-  // thread 0: this XCD's presence (the finish word's high half; complete before the workgroup
-  // counts itself finished) and the first claim; both latencies hide behind the routing
+  // thread 0: the first claim (its latency hides behind the routing); a workgroup's home XCD
+  // counter is nonzero from then on, which is how the last workgroup finds XCDs without any
   int pending = 0;
-  unsigned long long seen = 0;
-  if (threadIdx.x == 0) {
-    seen = atomicOr(finish, 1ull << (32 + home));
-    pending = atomicAdd(&claims[x], 1);
-  }
+  if (threadIdx.x == 0) pending = atomicAdd(&claims[x * kPipeLine], 1);
   const int ntasks = effective_tokens(ra.runtime_tokens, ra.host_tokens) * ra.topk;
   {
     const int wave = static_cast<int>(threadIdx.x) / kWave;
@@ -1420,7 +1416,6 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
   bool first_item = true;
   int present = -1;  // the last workgroup: XCDs that had workgroups (bit mask)
   int orphan = -1;   // the last workgroup: the XCD queue it runs
-  if (threadIdx.x == 0) asm volatile("" ::"v"(seen));  // the presence bit is set from here on
   for (;;) {
     if (threadIdx.x == 0) s_word = pending;
     __syncthreads();
@@ -1430,11 +1425,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
     const int ng = static_cast<int>(static_cast<int64_t>(G) * (x + 1) / kPipeXcds) - gb;
     if (t >= (n1 + n2) * ng) {
       if (present < 0) {
-        // count this workgroup finished; the last one learns which XCDs had workgroups
+        // count this workgroup finished (after its last claim was answered); the last one
+        // learns which XCDs had workgroups: those whose claim counter moved
         if (threadIdx.x == 0) {
-          const unsigned long long old = atomicAdd(finish, 1ull);
-          const bool is_last = static_cast<unsigned>(old & 0xffffffffull) == gridDim.x - 1;
-          s_word = is_last ? static_cast<int>((old >> 32) | (1ull << home)) : -1;
+          const bool is_last = atomicAdd(finish, 1) == static_cast<int>(gridDim.x) - 1;
+          int mask = -1;
+          if (is_last) {
+            mask = 0;
+            for (int q = 0; q < kPipeXcds; ++q)
+              if (__hip_atomic_load(&claims[q * kPipeLine], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+                mask |= 1 << q;
+          }
+          s_word = mask;
         }
         __syncthreads();
         present = s_word;
@@ -1445,10 +1447,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
       do ++orphan; while (orphan < kPipeXcds && ((present >> orphan) & 1));
       if (orphan >= kPipeXcds) break;
       x = orphan;
-      if (threadIdx.x == 0) pending = atomicAdd(&claims[x], 1);
+      if (threadIdx.x == 0) pending = atomicAdd(&claims[x * kPipeLine], 1);
       continue;
     }
-    if (threadIdx.x == 0) pending = atomicAdd(&claims[x], 1);  // the next claim, one item ahead
+    if (threadIdx.x == 0) pending = atomicAdd(&claims[x * kPipeLine], 1);  // the next claim, one item ahead
     const bool gemm1 = t < n1 * ng;
     const int local = gemm1 ? t : t - n1 * ng;
     const int per = gemm1 ? n1 : n2;
@@ -1496,7 +1498,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
   // claim was answered and its hand-off counts were done): the counters back to zero for the
   // next launch
   if (present >= 0)
-    for (int i = threadIdx.x; i < kPipeInts; i += kGemmThreads) p.pipe[i] = 0;
+    for (int i = threadIdx.x; i < kPipeHeader + G; i += kGemmThreads) p.pipe[i] = 0;
 }
 
 // Persistent dispatcher of the WIDE engine: every expert's rows as BM x 256 tiles, items dealt

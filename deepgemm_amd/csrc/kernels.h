@@ -168,10 +168,12 @@ hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream)
 // Decode pipeline (gemm.hip): GEMM1 with the in-kernel routing, the requant and GEMM2 of the
 // streaming engine in one launch, each group of rows handed from GEMM1 to GEMM2 inside its XCD.
 // pipe: kPipeInts counters, zero when the launch starts (its last workgroup zeroes them
-// again): [0..7] per-XCD claim counters, [8..9] the finish word (u64: finished workgroups |
-// XCDs that had workgroups << 32), [kPipeHeader..] GEMM1 items done per group.
+// again): the per-XCD claim counters at x * kPipeLine, the count of finished workgroups at
+// kPipeXcds * kPipeLine (each in a 128-byte line of its own: every workgroup's first claim and
+// its count-out go to them at about the same time), [kPipeHeader..] GEMM1 items done per group.
 constexpr int kPipeXcds = 8;
-constexpr int kPipeHeader = 16;
+constexpr int kPipeLine = 32;
+constexpr int kPipeHeader = (kPipeXcds + 1) * kPipeLine;
 constexpr int kMaxPipeGroups = 512;  // groups of <= 64 rows: S*K <= 8192 rows over <= 255 experts
 constexpr int kPipeInts = kPipeHeader + kMaxPipeGroups;
 struct PipeArgs {

@@ -108,7 +108,7 @@ typedef struct mmoe_scratch_layout {
 } mmoe_scratch_layout;
 
 #define MMOE_ROUTE_CHUNK 1024
-#define MMOE_PIPE_INTS 528
+#define MMOE_PIPE_INTS 800
 
 /* Arguments of one layer call. Replaces the argument list of fp8_mega_moe_impl,
  * csrc/apis/mega_dcu.hpp:338-354, and of
