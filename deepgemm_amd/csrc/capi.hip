@@ -397,9 +397,11 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     g2.direct_flag = direct_flag;
   }
 
-  // Decode (GEMM1 routes in-kernel): GEMM1, the requant and GEMM2 in one launch, each group of
-  // rows going on to GEMM2 as soon as its GEMM1 items are done. Its last workgroup sets its
-  // counters back to zero.
+  // Decode (GEMM1 routes in-kernel): GEMM1, the requant, GEMM2 and (when the call includes it)
+  // the combine in one launch, each group of rows going on to GEMM2 as soon as its GEMM1 items
+  // are done, each token combined as soon as its experts' GEMM2 items are. Its last workgroup
+  // sets its counters back to zero.
+  bool combined = false;
   if (route_in_gemm1 && runs(MMOE_STAGE_REQUANT) && runs(MMOE_STAGE_GEMM2) && !direct &&
       mmoe::decode_pipeline_supported(g1, g2, cus)) {
     mmoe::PipeArgs p;
@@ -413,6 +415,10 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     p.meta = at<int32_t>(ws, l.meta_offset);
     p.direct_flag = direct_flag;
     p.pipe = at<int32_t>(ws, l.pipe_offset);
+    if (runs(MMOE_STAGE_COMBINE) && a->hidden % 8 == 0 && a->hidden <= mmoe::kPipeCombineMaxHidden) {
+      p.y = static_cast<uint16_t*>(a->y);
+      combined = true;
+    }
     if (mmoe::launch_decode_pipeline(p, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   } else {
     if (runs(MMOE_STAGE_GEMM1) &&
@@ -434,7 +440,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
       return MMOE_ERR_HIP;
   }
 
-  if (runs(MMOE_STAGE_COMBINE)) {
+  if (runs(MMOE_STAGE_COMBINE) && !combined) {
     mmoe::CombineArgs c;
     memset(&c, 0, sizeof(c));
     c.y = static_cast<uint16_t*>(a->y);

@@ -196,7 +196,9 @@ __device__ __forceinline__ void publish_tile_scales(TileTables& tt, const TileSc
 // Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
 // the output (mrows <= 64; table row trow0 + r holds row r's scales), 64-column unit `unit`
 // of the output (SwiGLU: 32 channels).
-template <bool kSwiglu, int MT, bool kPmax = false>
+// kCoherent: the (GEMM2) stores go out device-coherent (sc1, written through the XCD's L2), so
+// that workgroups of other XCDs can read them in the same launch.
+template <bool kSwiglu, int MT, bool kPmax = false, bool kCoherent = false>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[MT][2], int row0,
                                            int mrows, int unit, const TileTables& tt, int trow0) {
   const int tid = opaque_tid();
@@ -221,8 +223,15 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[
       if (r >= mrows) continue;
       if (!kSwiglu) {
         uint16_t* crow = g.c + static_cast<int64_t>(row0 + r) * g.n + unit * 64 + rl;
-        crow[0] = f32_to_bf16(acc[mt][0][v] * xs[v] * b0);
-        crow[32] = f32_to_bf16(acc[mt][1][v] * xs[v] * b1);
+        const uint16_t c0 = f32_to_bf16(acc[mt][0][v] * xs[v] * b0);
+        const uint16_t c1 = f32_to_bf16(acc[mt][1][v] * xs[v] * b1);
+        if constexpr (kCoherent) {
+          __hip_atomic_store(crow, c0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(crow + 32, c1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          crow[0] = c0;
+          crow[32] = c1;
+        }
       } else {
         const float yv = swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs[v], b0, b1, rw[v]);
         g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl] = yv;
@@ -282,7 +291,7 @@ struct NoHook {
   __device__ __forceinline__ void operator()() const {}
 };
 template <bool kGather, bool kSwiglu, int MT, bool kFast, bool kEarly = false, bool kAResident = false,
-          bool kPmax = false, typename Hook = NoHook>
+          bool kPmax = false, bool kCoherent = false, typename Hook = NoHook>
 __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
                             uint8_t* smem, TileTables& tt, const Hook& before_a = Hook{}) {
   static_assert(!kAResident || (kEarly && kFast), "a resident A is staged by the hook");
@@ -427,7 +436,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
   }
 
   if (!active) return;
-  store_tile<kSwiglu, MT, kPmax>(g, acc, row0, mrows, unit, tt, 0);
+  store_tile<kSwiglu, MT, kPmax, kCoherent>(g, acc, row0, mrows, unit, tt, 0);
 }
 
 // ------------------------------------------------------------------ TILE engine
@@ -948,7 +957,8 @@ __device__ void fused_rows(const RouteArgs& a, int ntasks, int e, int cnt, int o
     if ((rank >= w_lo0 && rank < w_hi0) || (rank >= w_lo1 && rank < w_hi1)) {
       const int64_t row = static_cast<int64_t>(off_e) + rank;
       const int out = row < a.row_cap ? static_cast<int>(row) : -1;
-      a.output_index[task] = out;
+      // device-coherent: the decode pipeline's combine reads it from other XCDs
+      __hip_atomic_store(&a.output_index[task], out, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (out >= 0) {
         a.row_token[out] = s_tok[t];
         if (a.row_weight != nullptr) a.row_weight[out] = w;
@@ -1241,7 +1251,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 // waits on nothing, so every wait ends; a wait is also bounded (kPipeSpinLimit polls), and one
 // that runs out counts in meta[3] instead of hanging. The workgroup that finishes last runs the
 // queue of any XCD that no workgroup ran (none when the launch covers the chip), alone and
-// start to end, and then sets the counters back to zero.
+// start to end.
+//
+// Combine (PipeArgs::y set): a GEMM2 item stores its partial rows device-coherent (sc1: written
+// through the XCD's L2, which other XCDs do not see), drains them and counts itself done for its
+// expert. A workgroup out of items combines its share of the tokens, one wave a token: for each
+// routed slot (the task's expert from the routing's LDS table) it waits until the expert's
+// GEMM1 items are done (its rows' output_index entries are written, also device-coherent) and
+// loads the row, then until the expert's GEMM2 items are done, and reads the partial rows with
+// device-coherent loads. Every GEMM2 item is claimed by a workgroup of its XCD, or by the last
+// workgroup for an XCD without any, so every wait ends. The workgroup that leaves last sets the
+// counters back to zero.
 constexpr int kPipeSpinLimit = 1 << 20;  // polls of a group count (far longer than any item)
 
 __device__ __forceinline__ int hw_xcc_id() {
@@ -1263,6 +1283,84 @@ __device__ __forceinline__ bool wait_count(const int32_t* c, int target) {
     __builtin_amdgcn_s_sleep(2);
   }
   return false;
+}
+
+// One 16-byte piece at byte offset off of a buffer, device-coherent (sc1: an L2 line that another
+// XCD wrote is not served stale).
+__device__ __forceinline__ uint4 ld16_coherent(__amdgpu_buffer_rsrc_t r, int off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16 /* sc1 */);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// The combine of token t in the decode pipeline (one wave, whole rows of H <= 64 * 8 * 8
+// columns): the slot-ordered fp32 sum of its routed slots' partial rows from +0, bf16 RNE (the
+// combine kernel's arithmetic, so the same bits); a token without routed slots gets zeros.
+constexpr int kPipeCombineV = 8;  // 16-byte column groups per lane
+
+__device__ void pipe_combine_token(const PipeArgs& p, int64_t t, const uint8_t* s_ev,
+                                   const int* s_gprefix, int n1, int n2, const int32_t* done1,
+                                   const int32_t* done2, __amdgpu_buffer_rsrc_t part) {
+  constexpr int V = kPipeCombineV;
+  const RouteArgs& ra = p.g1.route;
+  const int lane = lane_id();
+  const int hidden = p.g2.n;
+  const int nvec = hidden >> 3;
+  int row = -1;
+  if (lane < ra.topk) {
+    const int64_t task = t * ra.topk + lane;
+    const int ev = s_ev[task];
+    if (ev != 255) {
+      bool ok = true;
+      for (int grp = s_gprefix[ev]; grp < s_gprefix[ev + 1]; ++grp) ok = ok && wait_count(&done1[grp], n1);
+      row = __hip_atomic_load(&ra.output_index[task], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = ok && wait_count(&done2[ev * kPipeDone2Stride], n2 * (s_gprefix[ev + 1] - s_gprefix[ev]));
+      if (!ok) atomicAdd(&p.meta[3], 1);
+    }
+  }
+  float sum[V][8];
+#pragma unroll
+  for (int j = 0; j < V; ++j)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sum[j][q] = 0.0f;
+  // the routed slots in ascending order, two at a time (their loads go out together)
+  constexpr int kSlots = 2;
+  for (uint64_t m = __ballot(row >= 0); m != 0;) {
+    uint4 pv[kSlots][V];
+    bool has[kSlots];
+#pragma unroll
+    for (int b = 0; b < kSlots; ++b) {
+      has[b] = m != 0;  // wave-uniform (a ballot)
+      const int s = has[b] ? __ffsll(static_cast<unsigned long long>(m)) - 1 : 0;
+      m &= m - 1;
+      const int r = __shfl(row, s, kWave);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int v = j * kWave + lane;
+        pv[b][j] = has[b] && v < nvec ? ld16_coherent(part, (r * hidden + v * 8) * 2) : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kSlots; ++b) {
+      if (!has[b]) break;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const uint32_t words[4] = {pv[b][j].x, pv[b][j].y, pv[b][j].z, pv[b][j].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          sum[j][2 * q] += bf16_to_f32(words[q] & 0xffff);
+          sum[j][2 * q + 1] += bf16_to_f32(words[q] >> 16);
+        }
+      }
+    }
+  }
+  uint4* yrow = reinterpret_cast<uint4*>(p.y + t * hidden);
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int v = j * kWave + lane;
+    if (v < nvec)
+      yrow[v] = make_uint4(pack_bf16x2(sum[j][0], sum[j][1]), pack_bf16x2(sum[j][2], sum[j][3]),
+                           pack_bf16x2(sum[j][4], sum[j][5]), pack_bf16x2(sum[j][6], sum[j][7]));
+  }
 }
 
 // Wave 0: s_gprefix[0..E] = exclusive prefix of the experts' groups (chunks of kStreamRows rows).
@@ -1372,8 +1470,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
   const RouteArgs& ra = g1.route;
   const int E = g1.num_experts;
   int32_t* const claims = p.pipe;  // XCD x's counter at claims[x * kPipeLine]
-  int32_t* const finish = p.pipe + kPipeXcds * kPipeLine;
-  int32_t* const done1 = p.pipe + kPipeHeader;  // [groups]
+  int32_t* const finish = p.pipe + kPipeFinishAt;
+  int32_t* const done1 = p.pipe + kPipeDone1At;  // [groups]
+  int32_t* const done2 = p.pipe + kPipeDone2At;  // [experts]
   const int hw = hw_xcc_id();
   const int home = hw & (kPipeXcds - 1);
   int x = home;
@@ -1488,17 +1587,39 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
         l1_invalidate();  // (a line of act_scale may hold another group's rows, read earlier)
       };
       const RowSrc rs{nullptr, nullptr, 0};
-      if (mrows > 32) stream_tile<false, false, 2, true, true, true>(g2, rs, e, row0, mrows, nb, smem, s_tt, stage_rows);
-      else stream_tile<false, false, 1, true, true, true>(g2, rs, e, row0, mrows, nb, smem, s_tt, stage_rows);
+      if (mrows > 32)
+        stream_tile<false, false, 2, true, true, true, false, true>(g2, rs, e, row0, mrows, nb, smem, s_tt, stage_rows);
+      else
+        stream_tile<false, false, 1, true, true, true, false, true>(g2, rs, e, row0, mrows, nb, smem, s_tt, stage_rows);
+      vm_drain();  // this wave's partial rows are written through to the device-coherent level
+      __syncthreads();
+      if (threadIdx.x == 0) atomicAdd(&done2[e * kPipeDone2Stride], 1);
     }
     first_item = false;
     __syncthreads();
   }
-  // the last workgroup, alone now (every other one has counted itself finished after its last
-  // claim was answered and its hand-off counts were done): the counters back to zero for the
-  // next launch
-  if (present >= 0)
+  if (p.y != nullptr && !too_many) {
+    // the combine: token i goes to wave (i / gridDim.x) % 8 of workgroup i % gridDim.x, so the
+    // tokens spread over all workgroups (each wave's tokens are independent of the others')
+    const int tokens = effective_tokens(ra.runtime_tokens, ra.host_tokens);
+    const int64_t part_bytes = static_cast<int64_t>(ra.row_cap) * g2.n * 2;
+    const __amdgpu_buffer_rsrc_t part = __builtin_amdgcn_make_buffer_rsrc(
+        g2.c, 0, static_cast<int>(part_bytes < 0x7fffffff ? part_bytes : 0x7fffffff), 0x00020000);
+    const int wave = static_cast<int>(threadIdx.x) / kWave;
+    for (int64_t t = blockIdx.x + static_cast<int64_t>(wave) * gridDim.x; t < tokens;
+         t += static_cast<int64_t>(gridDim.x) * kGemmWaves)
+      pipe_combine_token(p, t, s_ev, s_gprefix, n1, n2, done1, done2, part);
+  }
+  // the workgroup that leaves last (every other one has made its last counter access): the
+  // counters back to zero for the next launch
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_word = atomicAdd(p.pipe + kPipeExitAt, 1) == static_cast<int>(gridDim.x) - 1 ? 1 : 0;
+  __syncthreads();
+  if (s_word != 0) {
     for (int i = threadIdx.x; i < kPipeHeader + G; i += kGemmThreads) p.pipe[i] = 0;
+    for (int i = threadIdx.x; i < E; i += kGemmThreads) done2[i * kPipeDone2Stride] = 0;
+  }
 }
 
 // Persistent dispatcher of the WIDE engine: every expert's rows as BM x 256 tiles, items dealt

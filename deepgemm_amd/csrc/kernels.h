@@ -167,25 +167,36 @@ hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream)
 
 // Decode pipeline (gemm.hip): GEMM1 with the in-kernel routing, the requant and GEMM2 of the
 // streaming engine in one launch, each group of rows handed from GEMM1 to GEMM2 inside its XCD.
-// pipe: kPipeInts counters, zero when the launch starts (its last workgroup zeroes them
-// again): the per-XCD claim counters at x * kPipeLine, the count of finished workgroups at
-// kPipeXcds * kPipeLine (each in a 128-byte line of its own: every workgroup's first claim and
-// its count-out go to them at about the same time), [kPipeHeader..] GEMM1 items done per group.
+// pipe: kPipeInts counters, zero when the launch starts (its last workgroup to leave zeroes
+// them again), each header counter in a 128-byte line of its own (every workgroup goes to them
+// at about the same time): the per-XCD claim counters at x * kPipeLine, the count of workgroups
+// that ran out of items at kPipeFinishAt, the count of workgroups that left at kPipeExitAt;
+// then GEMM1 items done per group ([kPipeDone1At..], kMaxPipeGroups) and GEMM2 items done per
+// expert (expert e's at kPipeDone2At + e * kPipeDone2Stride: the combine's waves poll them).
 constexpr int kPipeXcds = 8;
 constexpr int kPipeLine = 32;
-constexpr int kPipeHeader = (kPipeXcds + 1) * kPipeLine;
+constexpr int kPipeFinishAt = kPipeXcds * kPipeLine;
+constexpr int kPipeExitAt = (kPipeXcds + 1) * kPipeLine;
+constexpr int kPipeHeader = (kPipeXcds + 2) * kPipeLine;
 constexpr int kMaxPipeGroups = 512;  // groups of <= 64 rows: S*K <= 8192 rows over <= 255 experts
-constexpr int kPipeInts = kPipeHeader + kMaxPipeGroups;
+constexpr int kMaxPipeExperts = 256;
+constexpr int kPipeDone1At = kPipeHeader;
+constexpr int kPipeDone2At = kPipeHeader + kMaxPipeGroups;
+constexpr int kPipeDone2Stride = 16;
+constexpr int kPipeInts = kPipeHeader + kMaxPipeGroups + kMaxPipeExperts * kPipeDone2Stride;
 struct PipeArgs {
   GemmArgs g1;           // GEMM1: route_in_kernel 1, SwiGLU epilogue into the fp32 y
-  GemmArgs g2;           // GEMM2: a = act, a_scale = act_scale
+  GemmArgs g2;           // GEMM2: a = act, a_scale = act_scale, c = the bf16 partial rows
   uint8_t* act;          // e4m3 [rows, I] (written by the first GEMM2 item of each group)
   float* act_scale;      // [rows]
   float* amax;           // [rows] (with act)
   int32_t* meta;         // [1] = 0 (the requant read y); [3] = bounded waits that ran out
   int32_t* direct_flag;  // set to 0 (no direct rows), or null
   int32_t* pipe;
+  uint16_t* y;           // non-null: the launch also runs the combine into y (bf16 [S, H];
+                         // H % 8 == 0 and H <= kPipeCombineMaxHidden)
 };
+constexpr int kPipeCombineMaxHidden = 64 * 8 * 8;  // one wave a token: 8 16-byte groups a lane
 bool decode_pipeline_supported(const GemmArgs& g1, const GemmArgs& g2, int num_cus);
 hipError_t launch_decode_pipeline(const PipeArgs& p, int num_cus, hipStream_t stream);
 

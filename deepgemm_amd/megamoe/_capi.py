@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_PKG_DIR, "libmegamoe_hip.so")
 MMOE_OK = 0
 MMOE_ERR_STATIC_SCRATCH = -15
 MMOE_STATIC_SCRATCH_BYTES = 128 << 20
-MMOE_PIPE_INTS = 800
+MMOE_PIPE_INTS = 4928
 MMOE_SCHEDULE_AUTO = 0
 MMOE_SCHEDULE_PERSISTENT = 1
 MMOE_SCHEDULE_STAGED = 2

@@ -101,14 +101,14 @@ typedef struct mmoe_scratch_layout {
                                   (GEMM1, GEMM2): zeroed by the routing stage, left at zero by
                                   the GEMMs themselves */
   int64_t pipe_offset;         /* int32 [MMOE_PIPE_INTS] counters of the one-launch decode
-                                  pipeline (GEMM1 + requant + GEMM2): zero when the scratch is
+                                  pipeline (GEMM1 + requant + GEMM2 + combine): zero when the scratch is
                                   new (allocate it zero-filled), and left zero by every call */
   int64_t pmax_offset;         /* f32   [min(rows, 8192), 2I/64] the decode pipeline's per-row
                                   max |y| of each 64-column block of GEMM1's output */
 } mmoe_scratch_layout;
 
 #define MMOE_ROUTE_CHUNK 1024
-#define MMOE_PIPE_INTS 800
+#define MMOE_PIPE_INTS 4928
 
 /* Arguments of one layer call. Replaces the argument list of fp8_mega_moe_impl,
  * csrc/apis/mega_dcu.hpp:338-354, and of
