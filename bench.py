@@ -65,8 +65,8 @@ def algorithmic_bytes(rows: int, touched: int) -> dict:
              + rows * (i + 4) * 2 + rows * h * 2)
     gemm1 = touched * 2 * i * h + touched * 2 * i * 4 + rows * (h + 4) + rows * 2 * i * 2
     gemm2 = touched * h * i + touched * h * 4 + rows * (i + 4) + rows * h * 2
-    # the decode pipeline runs both GEMMs (and the requant between them) in one launch
-    return dict(layer=layer, gemm1=gemm1, gemm2=gemm2, pipeline=gemm1 + gemm2)
+    # the decode pipeline runs the whole layer (routing through the combine) in one launch
+    return dict(layer=layer, gemm1=gemm1, gemm2=gemm2, pipeline=layer)
 
 
 # kernel names as rocprofv3 reports them: the 8-wave persistent kernel (decode-sized configs)
@@ -215,8 +215,8 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     def layer():
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf)
 
-    # the one-launch decode pipeline (routing, GEMM1, requant and GEMM2) is the only kernel that
-    # writes the per-block row maxima: whether it ran is read back from them
+    # the one-launch decode pipeline (routing, GEMM1, requant, GEMM2 and the combine) is the
+    # only kernel that writes the per-block row maxima: whether it ran is read back from them
     buf.scratch_view("pmax").fill_(-1.0)
     for _ in range(max(1, args.warmup)):
         layer()
@@ -246,15 +246,14 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     if not args.no_stage_timing:
         # The stages as the layer runs them: when GEMM1 routes in-kernel (small task counts)
         # routing and GEMM1 are one launch and are timed together.
-        # With the decode pipeline, routing through GEMM2 is one launch.
+        # With the decode pipeline the whole layer is one launch.
         call = mm.LayerCall(y, l1, l2, buf)
         fused_route = s * TOPK <= ROUTE_IN_GEMM1_MAX_TASKS
         if pipeline:
-            groups = [("pipeline", 0, 3)]
+            groups = [("pipeline", 0, 4)]
         else:
             groups = ([("gemm1", 0, 1)] if fused_route else [("route", 0, 0), ("gemm1", 1, 1)])
-            groups += [("requant", 2, 2), ("gemm2", 3, 3)]
-        groups += [("combine", 4, 4)]
+            groups += [("requant", 2, 2), ("gemm2", 3, 3), ("combine", 4, 4)]
         ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(groups) + 1)]
               for _ in range(args.steps)]
         for i in range(args.steps):
