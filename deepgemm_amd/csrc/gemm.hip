@@ -392,7 +392,8 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
     before_a();
     if constexpr (!kAResident) a_sources();
   }
-  const TileScaleRegs tsr = load_tile_scales<kGather, kSwiglu>(g, rs, e, row0, mrows, unit);
+  // a resident A's hook also leaves the rows' scales in tt.xs
+  const TileScaleRegs tsr = load_tile_scales<kGather, kSwiglu>(g, rs, e, row0, kAResident ? 0 : mrows, unit);
   load_chunk(0);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (!kEarly) {
@@ -403,7 +404,7 @@ __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0
     }
   }
   store_chunk(0);
-  publish_tile_scales(tt, tsr, mrows);
+  publish_tile_scales(tt, tsr, kAResident ? 0 : mrows);
   lds_barrier();
   for (int c = 0; c + 1 < nchunks; ++c) {
     load_chunk(c + 1);
@@ -1382,71 +1383,88 @@ __device__ void plan_groups(int E, const int* s_count, int* s_gprefix) {
 // MT = 1, two for MT = 2): the row's amax, inv = 448 / max(amax, 1e-4), then 16 e4m3 codes per
 // LDS piece -- the requant kernel's arithmetic, so the same bits. The amax is the max of the
 // row's 64 partial maxima that GEMM1's epilogue stored (one per 64-column block, exact), eight
-// lanes a row. Every workgroup of the group writes the rows' act_scale (the same values; the
-// tile's scale loads read them back); with write_act it also writes act and amax. The codes'
-// loads go out kStageBatch 16-byte pieces at a time.
+// lanes a row. The row scale a/448 goes straight into the tile's LDS scale table (s_xs); with
+// write_act the rows' act, act_scale and amax also go out. The y pieces go out kStageBatch at a
+// time, the first batch together with the maxima; rows past mrows are neither loaded nor
+// quantized (their LDS rows feed only accumulator rows that are never stored).
 constexpr int kStageBatch = 4;
 
 template <int MT>
 __device__ void stage_rows_from_y(const PipeArgs& p, int row0, int mrows, bool write_act,
-                                  uint8_t* smem, float* s_inv) {
+                                  uint8_t* smem, float* s_inv, float* s_xs) {
   constexpr int kc = kAChunk / (32 * MT);
   constexpr int kUnits = 2 * 2048 / kStreamUnit;  // partial maxima per row (I = 2048)
   static_assert(kStreamRows == kGemmWaves * kWave / 8, "eight lanes per row cover the group");
+  static_assert(kALoads % kStageBatch == 0, "whole batches");
   const int inter = p.g1.sw.inter;
   const int nchunks = inter / kc;
   const int tid = opaque_tid();
   const int lane = tid & (kWave - 1), wave = tid / kWave;
   const float* y = p.g1.sw.y;
-  {
-    const int r = tid >> 3, part = (tid & 7) * (kUnits / 8);
-    const float4* src = reinterpret_cast<const float4*>(
-        p.g1.row_pmax + static_cast<int64_t>(row0 + (r < mrows ? r : 0)) * kUnits + part);
-    float4 v[kUnits / 32];
+  const int r8 = tid >> 3;
+  float4 pm[kUnits / 32];
 #pragma unroll
-    for (int j = 0; j < kUnits / 32; ++j) v[j] = src[j];
+  for (int j = 0; j < kUnits / 32; ++j) pm[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (r8 < mrows) {
+    const float4* src = reinterpret_cast<const float4*>(
+        p.g1.row_pmax + static_cast<int64_t>(row0 + r8) * kUnits + (tid & 7) * (kUnits / 8));
+#pragma unroll
+    for (int j = 0; j < kUnits / 32; ++j) pm[j] = src[j];
+  }
+  // batch b of chunk c: pieces i = b * kStageBatch + h; piece i of a lane holds LDS bytes
+  // (i * 8 + wave) * 1024 + lane * 16 of the chunk buffer (row r, swizzled piece)
+  float4 v[kStageBatch][4];
+  auto load_batch = [&](int c, int b) {
+#pragma unroll
+    for (int h = 0; h < kStageBatch; ++h) {
+      const int pos = ((b * kStageBatch + h) * kGemmWaves + wave) * 1024 + lane * 16;
+      const int r = pos / kc;
+      const int off = c * kc + swizzle_piece((pos - r * kc) >> 4, r) * 16;
+      if (r < mrows) {
+        const float4* src = reinterpret_cast<const float4*>(y + static_cast<int64_t>(row0 + r) * inter + off);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[h][j] = src[j];
+      }
+    }
+  };
+  load_batch(0, 0);
+  {
     float m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kUnits / 32; ++j) m = fmaxf(fmaxf(fmaxf(m, v[j].x), fmaxf(v[j].y, v[j].z)), v[j].w);
+    for (int j = 0; j < kUnits / 32; ++j) m = fmaxf(fmaxf(fmaxf(m, pm[j].x), fmaxf(pm[j].y, pm[j].z)), pm[j].w);
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-    if ((tid & 7) == 0 && r < mrows) {
-      s_inv[r] = kE4m3Max / fmaxf(m, kAmaxFloor);
-      p.act_scale[row0 + r] = fmaxf(m, kAmaxFloor) / kE4m3Max;
-      if (write_act) p.amax[row0 + r] = m;
+    if ((tid & 7) == 0 && r8 < mrows) {
+      s_inv[r8] = kE4m3Max / fmaxf(m, kAmaxFloor);
+      s_xs[r8] = fmaxf(m, kAmaxFloor) / kE4m3Max;
+      if (write_act) {
+        p.act_scale[row0 + r8] = fmaxf(m, kAmaxFloor) / kE4m3Max;
+        p.amax[row0 + r8] = m;
+      }
     }
   }
   __syncthreads();
   for (int c = 0; c < nchunks; ++c) {
-    for (int i0 = 0; i0 < kALoads; i0 += kStageBatch) {
-      float4 v[kStageBatch][4];
-      int rr[kStageBatch], off[kStageBatch];
+    for (int b = 0; b < kALoads / kStageBatch; ++b) {
+      if (c > 0 || b > 0) load_batch(c, b);
 #pragma unroll
       for (int h = 0; h < kStageBatch; ++h) {
-        const int pos = ((i0 + h) * kGemmWaves + wave) * 1024 + lane * 16;
+        const int i = b * kStageBatch + h;
+        const int pos = (i * kGemmWaves + wave) * 1024 + lane * 16;
         const int r = pos / kc;
-        const int piece = swizzle_piece((pos - r * kc) >> 4, r);
-        rr[h] = r;
-        off[h] = c * kc + piece * 16;
-        const float4* src = reinterpret_cast<const float4*>(
-            y + static_cast<int64_t>(row0 + (r < mrows ? r : 0)) * inter + off[h]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[h][j] = src[j];
-      }
-#pragma unroll
-      for (int h = 0; h < kStageBatch; ++h) {
         int4 q = make_int4(0, 0, 0, 0);  // rows past mrows: never stored
-        if (rr[h] < mrows) {
-          const float inv = s_inv[rr[h]];
+        if (r < mrows) {
+          const float inv = s_inv[r];
           q.x = static_cast<int>(pack_e4m3x4(v[h][0].x * inv, v[h][0].y * inv, v[h][0].z * inv, v[h][0].w * inv));
           q.y = static_cast<int>(pack_e4m3x4(v[h][1].x * inv, v[h][1].y * inv, v[h][1].z * inv, v[h][1].w * inv));
           q.z = static_cast<int>(pack_e4m3x4(v[h][2].x * inv, v[h][2].y * inv, v[h][2].z * inv, v[h][2].w * inv));
           q.w = static_cast<int>(pack_e4m3x4(v[h][3].x * inv, v[h][3].y * inv, v[h][3].z * inv, v[h][3].w * inv));
-          if (write_act)
-            *reinterpret_cast<int4*>(p.act + static_cast<int64_t>(row0 + rr[h]) * inter + off[h]) = q;
+          if (write_act) {
+            const int off = c * kc + swizzle_piece((pos - r * kc) >> 4, r) * 16;
+            *reinterpret_cast<int4*>(p.act + static_cast<int64_t>(row0 + r) * inter + off) = q;
+          }
         }
-        *reinterpret_cast<int4*>(smem + (c & 1) * kAChunk + wave * 1024 + lane * 16 +
-                                 (i0 + h) * kGemmWaves * 1024) = q;
+        *reinterpret_cast<int4*>(smem + (c & 1) * kAChunk + wave * 1024 + lane * 16 + i * kGemmWaves * 1024) = q;
       }
     }
   }
@@ -1580,11 +1598,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
         if (threadIdx.x == 0 && !wait_count(&done1[grp], n1)) atomicAdd(&p.meta[3], 1);
         __syncthreads();
         l1_invalidate();
-        if (mrows > 32) stage_rows_from_y<2>(p, row0, mrows, nb == 0, smem, s_inv);
-        else stage_rows_from_y<1>(p, row0, mrows, nb == 0, smem, s_inv);
-        vm_drain();  // act_scale is read back by the tile's scale loads
+        if (mrows > 32) stage_rows_from_y<2>(p, row0, mrows, nb == 0, smem, s_inv, s_tt.xs);
+        else stage_rows_from_y<1>(p, row0, mrows, nb == 0, smem, s_inv, s_tt.xs);
         __syncthreads();
-        l1_invalidate();  // (a line of act_scale may hold another group's rows, read earlier)
       };
       const RowSrc rs{nullptr, nullptr, 0};
       if (mrows > 32)
