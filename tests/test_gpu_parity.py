@@ -641,8 +641,10 @@ def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
 
 def test_graph_full_shape_both_kernels(mm, cuda, full_weights):
     """The production shape in a 2048-token bucket (every slot local: a WIDE row bound): a full
-    replay runs the WIDE kernels, a short one the 8-wave kernels with GEMM1 routing in-kernel;
-    both are bitwise equal to eager calls on the same prefix."""
+    replay runs the WIDE kernels, a short one the 8-wave kernels with GEMM1 routing in-kernel,
+    also on both sides of the in-kernel routing's task limit (1365 tokens = 8190 tasks: 8-wave;
+    1366 = 8196: WIDE). Every replay is bitwise equal to an eager call on the same prefix, and
+    rows past it are left alone."""
     l1, l2 = full_weights[0], full_weights[1]
     s_max = 2048
     x_fp8, x_sf, idx, w = make_tokens(s_max, 4096, 32, 6, seed=333, global_experts=None)
@@ -657,7 +659,7 @@ def test_graph_full_shape_both_kernels(mm, cuda, full_weights):
     with torch.cuda.graph(graph):
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
     ref_buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
-    for n, wide in ((s_max, True), (100, False)):
+    for n, wide in ((s_max, True), (100, False), (1365, False), (1366, True), (100, False)):
         log(f"  replay with runtime tokens={n}")
         y.fill_(7.0)
         buf.cuda_graph_num_tokens.fill_(n)
