@@ -196,8 +196,11 @@ __device__ __forceinline__ void publish_tile_scales(TileTables& tt, const TileSc
 // Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
 // the output (mrows <= 64; table row trow0 + r holds row r's scales), 64-column unit `unit`
 // of the output (SwiGLU: 32 channels).
-// kCoherent: the (GEMM2) stores go out device-coherent (sc1, written through the XCD's L2), so
-// that workgroups of other XCDs can read them in the same launch.
+// kCoherent: the stores go out device-coherent (sc1, written through the XCD's L2): GEMM2's
+// partial rows, so that workgroups of other XCDs can read them in the same launch, and GEMM1's
+// fp32 SwiGLU rows of the decode pipeline, which its GEMM2 items of the same XCD still read from
+// L2 but which no longer sit there dirty (c1 150.9 -> 148.9 us per layer; its y output rows
+// written through as well made no difference, its act rows as 4-byte coherent stores +3 us).
 template <bool kSwiglu, int MT, bool kPmax = false, bool kCoherent = false>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[MT][2], int row0,
                                            int mrows, int unit, const TileTables& tt, int trow0) {
@@ -234,7 +237,11 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[
         }
       } else {
         const float yv = swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs[v], b0, b1, rw[v]);
-        g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl] = yv;
+        if constexpr (kCoherent)
+          __hip_atomic_store(&g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl], yv,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl] = yv;
         pm[v] = fabsf(yv);
       }
     }
@@ -1587,8 +1594,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
                    nb == 0 ? r0 + kStreamRows : 0, 0, 0, s_task, s_tok, s_rw);
       };
       const RowSrc rs{s_tok, s_rw, row0};
-      if (mrows > 32) stream_tile<true, true, 2, true, true, false, true>(g1, rs, e, row0, mrows, nb, smem, s_tt, rank_rows);
-      else stream_tile<true, true, 1, true, true, false, true>(g1, rs, e, row0, mrows, nb, smem, s_tt, rank_rows);
+      if (mrows > 32) stream_tile<true, true, 2, true, true, false, true, true>(g1, rs, e, row0, mrows, nb, smem, s_tt, rank_rows);
+      else stream_tile<true, true, 1, true, true, false, true, true>(g1, rs, e, row0, mrows, nb, smem, s_tt, rank_rows);
       vm_drain();  // this wave's y stores are in L2
       __syncthreads();
       if (threadIdx.x == 0) atomicAdd(&done1[grp], 1);
