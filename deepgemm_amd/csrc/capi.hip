@@ -421,22 +421,28 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     }
     if (mmoe::launch_decode_pipeline(p, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   } else {
+    // Eager calls whose bound selects WIDE by a small margin: the routing's row count chooses
+    // between WIDE and the 8-wave kernels on the device as well (gemm_eager_dual), with a
+    // threshold of its own (these calls never route in GEMM1).
+    const bool eager_dual = a->runtime_num_tokens == nullptr && mmoe::gemm_eager_dual(g1, max_rows);
+    const int32_t* dual_rows = eager_dual ? at<int32_t>(ws, l.meta_offset) : rows_on_device;
+    const int dual_min = eager_dual ? mmoe::gemm_eager_dual_min_rows(a->num_experts)
+                                    : mmoe::gemm_wide_min_rows(a->num_experts);
     if (runs(MMOE_STAGE_GEMM1) &&
-        mmoe::launch_grouped_gemm(g1, max_rows, cus, s, rows_on_device, route_small_in_gemm1) != hipSuccess)
+        mmoe::launch_grouped_gemm(g1, max_rows, cus, s, dual_rows, route_small_in_gemm1, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
     // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU (after
     // a dual GEMM1 launch it finds out on the device which GEMM1 ran)
     const bool wide1 = mmoe::gemm_wide_selected(g1, max_rows);
-    const bool dual1 = wide1 && rows_on_device != nullptr;
+    const bool dual1 = wide1 && dual_rows != nullptr;
     if (runs(MMOE_STAGE_REQUANT) &&
         mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, g1.sw, at<float>(ws, l.amax_offset),
                              at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
                              at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, dest,
-                             cus, s, dual1 ? rows_on_device : nullptr,
-                             mmoe::gemm_wide_min_rows(a->num_experts)) != hipSuccess)
+                             cus, s, dual1 ? dual_rows : nullptr, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
     if (runs(MMOE_STAGE_GEMM2) &&
-        mmoe::launch_grouped_gemm(g2, max_rows, cus, s, rows_on_device) != hipSuccess)
+        mmoe::launch_grouped_gemm(g2, max_rows, cus, s, dual_rows, false, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
   }
 

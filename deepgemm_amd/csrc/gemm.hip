@@ -1824,6 +1824,20 @@ int gemm_wide_min_rows(int num_experts) {
   return std::max(kFusedMaxTasks + 1, kWideMinRowsPerExpert * num_experts);
 }
 
+// Eager calls whose row bound selects WIDE only by a small margin: the routed rows may be far
+// fewer (an EP share keeps ~1/8 of its slots), so both kernels go out and the rows choose on the
+// device -- the 8-wave kernels (each expert's weights streamed once by the STREAM engine while
+// experts have at most 64 rows) below an average of 64 rows an expert, WIDE from there. Measured
+// at T = 192..2048 a rank (256 global experts): 36 and 46 rows an expert ran 181/183 us on the
+// 8-wave kernels against 224/226 us on WIDE; 72 and 97 rows 242/266 against 229/239 us. Above
+// 16 x that many tasks the bound selects WIDE directly (no launches that return at once).
+constexpr int kEagerDualRowsPerExpert = kStreamRows;
+int gemm_eager_dual_min_rows(int num_experts) { return kEagerDualRowsPerExpert * num_experts; }
+bool gemm_eager_dual(const GemmArgs& g, int max_rows) {
+  return gemm_wide_selected(g, max_rows) &&
+         static_cast<int64_t>(max_rows) < 16ll * gemm_eager_dual_min_rows(g.num_experts);
+}
+
 // The decode pipeline needs the streaming engine's full-chunk shapes for both GEMMs (GEMM2's
 // K = I in at most two chunks, staged whole by the requant), GEMM1's in-kernel routing, and
 // the whole MI355X (8 XCDs of 32 CUs: its queues are the hardware XCD ids).
@@ -1849,7 +1863,8 @@ hipError_t launch_decode_pipeline(const PipeArgs& p, int num_cus, hipStream_t st
 }
 
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream,
-                               const int32_t* rows_on_device, bool route_small_in_kernel) {
+                               const int32_t* rows_on_device, bool route_small_in_kernel,
+                               int dual_min_rows) {
   if (max_rows <= 0) return hipSuccess;
   if (g.num_experts > kMaxGemmExperts || g.dual_rows != nullptr) return hipErrorInvalidValue;
   const bool wide = gemm_wide_selected(g, max_rows);
@@ -1872,7 +1887,9 @@ hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hip
     // WIDE GEMM2's direct writes, which the requant then leaves switched off)
     GemmArgs d = g;
     d.dual_rows = rows_on_device;
-    d.dual_min_rows = gemm_wide_min_rows(g.num_experts);
+    d.dual_min_rows = dual_min_rows > 0 ? dual_min_rows : gemm_wide_min_rows(g.num_experts);
+    // (a smaller threshold than the default only where the 8-wave kernel never routes itself)
+    if (d.dual_min_rows <= kFusedMaxTasks && route_small_in_kernel) return hipErrorInvalidValue;
     eight.dual_rows = d.dual_rows;
     eight.dual_min_rows = d.dual_min_rows;
     eight.row_dest = nullptr;

@@ -112,9 +112,15 @@ constexpr int kSchedInts = 16;
 // (RouteArgs::fused_max_tasks).
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream,
                                const int32_t* rows_on_device = nullptr,
-                               bool route_small_in_kernel = false);
-// The routed-row count from which the WIDE kernel is chosen on the device (dual launches).
+                               bool route_small_in_kernel = false, int dual_min_rows = 0);
+// The routed-row count from which the WIDE kernel is chosen on the device (dual launches of
+// graph replays; dual_min_rows 0 selects it).
 int gemm_wide_min_rows(int num_experts);
+// Eager calls: true when the row bound selects WIDE but the routed rows should choose on the
+// device (a dual launch with rows_on_device = the routing's meta[0] and dual_min_rows =
+// gemm_eager_dual_min_rows: WIDE from an average of 64 rows an expert).
+bool gemm_eager_dual(const GemmArgs& g, int max_rows);
+int gemm_eager_dual_min_rows(int num_experts);
 bool gemm_shape_supported(int n, int k);
 // True when launch_grouped_gemm runs the WIDE kernel for g: GEMM1 then writes the bf16
 // pre-activation h [rows, 2I] instead of the SwiGLU output y (requant computes the SwiGLU).

@@ -246,6 +246,11 @@ FULL_SHAPE_CASES = {
     "ragged_77": (77, 64, None, "8wave"),
     "clamp10": (96, None, 10.0, "8wave"),
     "wide_2048": (2048, None, None, "wide"),
+    # eager calls whose task bound selects WIDE by a small margin: the routed rows choose on the
+    # device (an EP share of 2048 tokens keeps ~1500 rows: the 8-wave kernels; of 4096, ~3100:
+    # WIDE, from 64 rows an expert)
+    "ep_2048": (2048, 256, None, "8wave"),
+    "ep_4096": (4096, 256, None, "wide"),
     # clamp 1.0 binds on both sides of the gate and of the up value (h ~ N(0, 1)): the 8-wave
     # epilogue on the STREAM engine (c1 routing), on the TILE engine (Zipf: experts with more
     # than 64 rows), and the WIDE kernel's requant from h
