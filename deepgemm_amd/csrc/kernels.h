@@ -171,8 +171,9 @@ struct CombineArgs {
 };
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream);
 
-// Decode pipeline (gemm.hip): GEMM1 with the in-kernel routing, the requant and GEMM2 of the
-// streaming engine in one launch, each group of rows handed from GEMM1 to GEMM2 inside its XCD.
+// Decode pipeline (gemm.hip): GEMM1 with the in-kernel routing, the requant, GEMM2 of the
+// streaming engine and (PipeArgs::y) the combine in one launch, each group of rows handed from
+// GEMM1 to GEMM2 inside its XCD, each token combined once its experts' GEMM2 items are done.
 // pipe: kPipeInts counters, zero when the launch starts (its last workgroup to leave zeroes
 // them again), each header counter in a 128-byte line of its own (every workgroup goes to them
 // at about the same time): the per-XCD claim counters at x * kPipeLine, the count of workgroups
