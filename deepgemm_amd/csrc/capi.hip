@@ -421,12 +421,12 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     }
     if (mmoe::launch_decode_pipeline(p, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   } else {
-    // Eager calls whose bound selects WIDE by a small margin: the routing's row count chooses
-    // between WIDE and the 8-wave kernels on the device as well (gemm_eager_dual), with a
-    // threshold of its own (these calls never route in GEMM1).
+    // Eager calls whose bound selects WIDE by a small margin: the routing's largest expert row
+    // count (meta[4]) chooses between WIDE and the 8-wave kernels on the device as well
+    // (gemm_eager_dual; these calls never route in GEMM1).
     const bool eager_dual = a->runtime_num_tokens == nullptr && mmoe::gemm_eager_dual(g1, max_rows);
-    const int32_t* dual_rows = eager_dual ? at<int32_t>(ws, l.meta_offset) : rows_on_device;
-    const int dual_min = eager_dual ? mmoe::gemm_eager_dual_min_rows(a->num_experts)
+    const int32_t* dual_rows = eager_dual ? at<int32_t>(ws, l.meta_offset) + 4 : rows_on_device;
+    const int dual_min = eager_dual ? mmoe::gemm_eager_dual_min_largest()
                                     : mmoe::gemm_wide_min_rows(a->num_experts);
     if (runs(MMOE_STAGE_GEMM1) &&
         mmoe::launch_grouped_gemm(g1, max_rows, cus, s, dual_rows, route_small_in_gemm1, dual_min) != hipSuccess)

@@ -78,6 +78,12 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+__device__ __forceinline__ int wave_max(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
 // Max of v >= 0 over each half-wave (lanes 0-31, 32-63), valid in lanes 16-31 and 48-63 (all
 // lanes active), by DPP: quad swaps, half-row and row mirrors give every lane its 16-lane row's
 // max, then row_bcast:15 brings row 0's max into row 1 and row 2's into row 3 (other rows: 0).

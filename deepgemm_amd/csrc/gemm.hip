@@ -1825,17 +1825,19 @@ int gemm_wide_min_rows(int num_experts) {
 }
 
 // Eager calls whose row bound selects WIDE only by a small margin: the routed rows may be far
-// fewer (an EP share keeps ~1/8 of its slots), so both kernels go out and the rows choose on the
-// device -- the 8-wave kernels (each expert's weights streamed once by the STREAM engine while
-// experts have at most 64 rows) below an average of 64 rows an expert, WIDE from there. Measured
-// at T = 192..2048 a rank (256 global experts): 36 and 46 rows an expert ran 181/183 us on the
-// 8-wave kernels against 224/226 us on WIDE; 72 and 97 rows 242/266 against 229/239 us. Above
-// 16 x that many tasks the bound selects WIDE directly (no launches that return at once).
-constexpr int kEagerDualRowsPerExpert = kStreamRows;
-int gemm_eager_dual_min_rows(int num_experts) { return kEagerDualRowsPerExpert * num_experts; }
+// fewer (an EP share keeps ~1/8 of its slots), so both kernels go out and the routing's largest
+// expert row count chooses on the device -- the 8-wave kernels while every expert has at most
+// 64 rows (each expert's weights streamed once by the STREAM engine), WIDE from 65 (the
+// STREAM engine would stream some experts' weights twice). Measured on the 8-wave kernels at
+// T = 224..352 a rank (256 global experts, 42..67 rows an expert on average): 181-183 us while
+// the largest expert fits 64 rows, 230-241 us once it does not, against 224-232 us on WIDE.
+// Auto schedules only (an engine set by the caller keeps its kernels); above 16 x 64 tasks an
+// expert the bound selects WIDE directly (no launches that return at once).
+constexpr int kEagerDualMinLargest = kStreamRows + 1;
+int gemm_eager_dual_min_largest() { return kEagerDualMinLargest; }
 bool gemm_eager_dual(const GemmArgs& g, int max_rows) {
-  return gemm_wide_selected(g, max_rows) &&
-         static_cast<int64_t>(max_rows) < 16ll * gemm_eager_dual_min_rows(g.num_experts);
+  return g.engine == GemmEngine::kAuto && gemm_wide_selected(g, max_rows) &&
+         static_cast<int64_t>(max_rows) < 16ll * kStreamRows * g.num_experts;
 }
 
 // The decode pipeline needs the streaming engine's full-chunk shapes for both GEMMs (GEMM2's

@@ -92,7 +92,8 @@ struct GemmArgs {
   // Set by launch_grouped_gemm for a row bound that selects the WIDE kernel while the actual rows
   // are only known on the device (graph replays): the 8-wave and the WIDE kernel are both
   // launched, and each returns at once unless the routed rows (*dual_rows, the routing's
-  // meta[0]) select it -- WIDE at dual_min_rows or more. Null: the launch always runs.
+  // meta[0], or its meta[4] for eager calls) select it -- WIDE at dual_min_rows or more.
+  // Null: the launch always runs.
   const int32_t* dual_rows;
   int dual_min_rows;
   // Decode pipeline GEMM1: per row, the max |SwiGLU output| of each 64-column unit (float
@@ -116,11 +117,12 @@ hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hip
 // The routed-row count from which the WIDE kernel is chosen on the device (dual launches of
 // graph replays; dual_min_rows 0 selects it).
 int gemm_wide_min_rows(int num_experts);
-// Eager calls: true when the row bound selects WIDE but the routed rows should choose on the
-// device (a dual launch with rows_on_device = the routing's meta[0] and dual_min_rows =
-// gemm_eager_dual_min_rows: WIDE from an average of 64 rows an expert).
+// Eager calls on the auto schedule: true when the row bound selects WIDE but the routed rows
+// should choose on the device (a dual launch with rows_on_device = the routing's meta[4], the
+// largest expert's row count, and dual_min_rows = gemm_eager_dual_min_largest: WIDE once an
+// expert has more than 64 rows).
 bool gemm_eager_dual(const GemmArgs& g, int max_rows);
-int gemm_eager_dual_min_rows(int num_experts);
+int gemm_eager_dual_min_largest();
 bool gemm_shape_supported(int n, int k);
 // True when launch_grouped_gemm runs the WIDE kernel for g: GEMM1 then writes the bf16
 // pre-activation h [rows, 2I] instead of the SwiGLU output y (requant computes the SwiGLU).

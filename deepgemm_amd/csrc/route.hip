@@ -90,11 +90,12 @@ __device__ void wave_route(const RouteArgs& a, int64_t begin, int64_t end, int* 
 
 // Expert offsets from totals (exclusive scan, or the caller's counts for the preprocess), by
 // wave 0 in 64-expert chunks (DPP scans); fills s_off[0..E], and the writer workgroup
-// publishes offsets, counts, stats and the routed row count.
+// publishes offsets, counts, stats, the routed row count (meta[0]) and the largest expert's
+// row count (meta[4]).
 __device__ void publish_offsets(const RouteArgs& a, const int* s_tot, int* s_off, bool writer) {
   if (threadIdx.x < kWave) {
     const int lane = lane_id();
-    int carry = 0, routed = 0;
+    int carry = 0, routed = 0, largest = 0;
     for (int e0 = 0; e0 < a.num_experts; e0 += kWave) {
       const int e = e0 + lane;
       const int tot = e < a.num_experts ? s_tot[e] : 0;
@@ -103,10 +104,14 @@ __device__ void publish_offsets(const RouteArgs& a, const int* s_tot, int* s_off
       if (e < a.num_experts) s_off[e] = carry + inc - c;
       carry += __shfl(inc, kWave - 1, kWave);
       routed += __shfl(wave_inclusive_sum(tot), kWave - 1, kWave);
+      largest = max(largest, wave_max(tot));
     }
     if (lane == 0) {
       s_off[a.num_experts] = carry;
-      if (writer) a.meta[0] = static_cast<int32_t>(routed < a.row_cap ? routed : a.row_cap);
+      if (writer) {
+        a.meta[0] = static_cast<int32_t>(routed < a.row_cap ? routed : a.row_cap);
+        a.meta[4] = largest;
+      }
     }
   }
   __syncthreads();

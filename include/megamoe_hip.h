@@ -81,7 +81,8 @@ typedef struct mmoe_scratch_layout {
   int64_t offsets_offset;      /* int32 [E+1] first row of each expert (exclusive scan) */
   int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R; [1] = 1: GEMM1 left
                                   the bf16 pre-activation h in y's bytes; [2] = 1: GEMM2 wrote
-                                  the rows of single-slot tokens straight to y (row_dest) */
+                                  the rows of single-slot tokens straight to y (row_dest);
+                                  [4] = the largest expert's row count (routing launches) */
   int64_t chunk_counts_offset; /* int32 [num_chunks, E] per-chunk counts, then
                                   [num_chunks, 16, E] per-wave counts (routing) */
   int64_t output_index_offset; /* int32 [S_max, K]  row of (token, slot) or -1 */

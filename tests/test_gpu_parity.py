@@ -246,10 +246,12 @@ FULL_SHAPE_CASES = {
     "ragged_77": (77, 64, None, "8wave"),
     "clamp10": (96, None, 10.0, "8wave"),
     "wide_2048": (2048, None, None, "wide"),
-    # eager calls whose task bound selects WIDE by a small margin: the routed rows choose on the
-    # device (an EP share of 2048 tokens keeps ~1500 rows: the 8-wave kernels; of 4096, ~3100:
-    # WIDE, from 64 rows an expert)
+    # eager calls whose task bound selects WIDE by a small margin: the routing's largest expert
+    # row count chooses on the device (an EP share of 2048 tokens: 1555 rows, at most 63 an
+    # expert -> the 8-wave kernels; of 2304: 1697 rows, 53 an expert on average but 68 in the
+    # largest -> WIDE; of 4096: 3046 rows -> WIDE)
     "ep_2048": (2048, 256, None, "8wave"),
+    "ep_2304": (2304, 256, None, "wide"),
     "ep_4096": (4096, 256, None, "wide"),
     # clamp 1.0 binds on both sides of the gate and of the up value (h ~ N(0, 1)): the 8-wave
     # epilogue on the STREAM engine (c1 routing), on the TILE engine (Zipf: experts with more
@@ -291,6 +293,8 @@ def test_layer_full_shape(mm, cuda, full_weights, case):
     assert np.array_equal(stats.cpu().numpy(), tr.routing.counts)
     assert (buf.scratch_view("meta")[1].item() == 1) == (kernel == "wide")
     assert (buf.scratch_view("meta")[2].item() == 1) == (kernel == "wide")
+    if case.startswith("ep_"):  # the routing launch's largest expert row count
+        assert buf.scratch_view("meta")[4].item() == int(tr.routing.counts.max())
     if clamp is not None and clamp < 5.0:
         _assert_clamp_binds(tr.h, clamp)
     if g == "zipf":  # the TILE engine: experts with more than 64 rows next to small ones
