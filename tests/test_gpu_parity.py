@@ -330,6 +330,29 @@ def test_layer_every_schedule_matches_oracle_and_is_deterministic(mm, cuda, full
     assert d <= CALC_DIFF_BAR
 
 
+@pytest.mark.parametrize("mode,wide", [("auto", False), ("1", True), ("0", False)])
+def test_eager_dual_applies_to_the_auto_schedule_only(mm, cuda, full_weights, monkeypatch, mode, wide):
+    """An EP share of 2048 tokens (1555 routed rows, at most 63 an expert; the task bound selects
+    WIDE): the auto schedule's dual launch lets the routing choose the 8-wave kernels, while a
+    caller-set engine keeps the host's choice -- WIDE for the tile engine (=1), the streaming
+    engine for =0 (which never selects WIDE). Each meets the bar against the oracle."""
+    l1, l2, l1c, l2c, unpacked = full_weights
+    s = 2048
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, global_experts=256)
+    monkeypatch.setenv("MEGAMOE_DCU_USE_LARGE_OPT_3STAGE", mode)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
+    log(f"eager dual: schedule mode={mode}")
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    meta = buf.scratch_view("meta")
+    assert (meta[1].item() == 1) == wide, "WIDE GEMM1 (bf16 h) exactly when expected"
+    tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, unpacked_weights=unpacked)
+    assert int(tr.routing.counts.max()) <= 64
+    d = O.calc_diff(y.cpu(), tr.y)
+    log(f"  calc_diff={d:.3e}")
+    assert d <= CALC_DIFF_BAR
+
+
 @pytest.mark.parametrize("s", [512, 2048])
 def test_layer_zipf_empty_experts(mm, cuda, full_weights, s):
     l1, l2, l1c, l2c, unpacked = full_weights
