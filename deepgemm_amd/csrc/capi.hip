@@ -364,9 +364,25 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     g1.route = forward_route_args(a, l);
   }
   if (route_small_in_gemm1) g1.route = forward_route_args(a, l);
+  // Whole-layer calls on the WIDE GEMM1: its workgroups out of tiles write the zero y rows of
+  // tokens without a valid routed slot, and the combine skips them. The routing launch of the
+  // same call zeroes the claim counter (also when it returns at once).
+  const bool zero_fill = runs(MMOE_STAGE_ROUTE) && !route_in_gemm1 && runs(MMOE_STAGE_COMBINE) &&
+                         a->hidden % 8 == 0 && mmoe::gemm_wide_selected(g1, max_rows);
+  int32_t* zfill_claim = at<int32_t>(ws, l.sched_offset) + mmoe::kZeroFillClaim;
+  if (zero_fill) {
+    g1.zf.y = static_cast<uint16_t*>(a->y);
+    g1.zf.claim = zfill_claim;
+    g1.zf.output_index = at<int32_t>(ws, l.output_index_offset);
+    g1.zf.runtime_tokens = a->runtime_num_tokens;
+    g1.zf.host_tokens = a->num_tokens;
+    g1.zf.topk = a->num_topk;
+    g1.zf.hidden = a->hidden;
+  }
 
   mmoe::GemmArgs g2 = g1;
   memset(&g2.sw, 0, sizeof(g2.sw));
+  memset(&g2.zf, 0, sizeof(g2.zf));
   g2.route_in_kernel = 0;
   g2.a = at<uint8_t>(ws, l.act_offset);
   g2.row_token = nullptr;
@@ -457,6 +473,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     c.topk = a->num_topk;
     c.hidden = a->hidden;
     c.skip_single = direct_flag;
+    if (zero_fill) c.zfill_claim = zfill_claim;
     if (mmoe::launch_combine(c, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   }
   return MMOE_OK;

@@ -168,13 +168,20 @@ __global__ __launch_bounds__(kEltThreads) void combine_kernel(CombineArgs c) {
     return row;
   };
   const bool skip_single = c.skip_single != nullptr && *c.skip_single != 0;
+  // tokens below zdone without a routed slot: GEMM1 wrote their zero rows (ZeroFill)
+  int64_t zdone = 0;
+  if (c.zfill_claim != nullptr) {
+    const int64_t claimed = *c.zfill_claim;
+    const int64_t nchunks = (tokens + kZeroFillTokens - 1) / kZeroFillTokens;
+    zdone = (claimed < nchunks ? claimed : nchunks) * kZeroFillTokens;
+  }
   float w;
   int row = slot_row(it, w);
   for (; it < items; it += stride) {
     float next_w;
     const int next_row = slot_row(it + stride, next_w);
     const uint64_t routed = __ballot(row >= 0);
-    if (!(skip_single && __popcll(routed) == 1)) {
+    if (!(skip_single && __popcll(routed) == 1) && !(routed == 0 && it / parts < zdone)) {
       const int64_t t = it / parts;
       const int v0 = static_cast<int>(it - t * parts) * kWave * V;
       float sum[V][8];

@@ -1729,6 +1729,37 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
     }
     __syncthreads();
   }
+  if (kSwiglu && g.zf.y != nullptr && !dynamic) {
+    // out of tiles: the zero y rows of tokens without a valid routed slot, a claimed chunk of
+    // kZeroFillTokens tokens at a time (a wave a token), while other workgroups still run tiles
+    // (claim[1] counts the workgroups out of tiles); the combine writes the chunks left. Only
+    // with the static deal (many tiles a workgroup): with claimed tiles the idle end is short,
+    // and the zero rows' writes slowed the last tiles by more than the combine saved (c2: +28 us
+    // per layer; c3: -60 us).
+    const ZeroFill& z = g.zf;
+    const int tokens = effective_tokens(z.runtime_tokens, z.host_tokens);
+    const int nchunks = (tokens + kZeroFillTokens - 1) / kZeroFillTokens;
+    const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
+    const int nvec = z.hidden >> 3;
+    if (threadIdx.x == 0) atomicAdd(z.claim + 1, 1);
+    for (;;) {
+      __syncthreads();  // every thread has read s_item
+      if (threadIdx.x == 0) {
+        const int idle = __hip_atomic_load(z.claim + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_item = idle >= static_cast<int>(gridDim.x) ? nchunks : atomicAdd(z.claim, 1);
+      }
+      __syncthreads();
+      const int c = s_item;
+      if (c >= nchunks) break;
+      const int t_end = min(tokens, (c + 1) * kZeroFillTokens);
+      for (int t = c * kZeroFillTokens + wave; t < t_end; t += kWideWaves) {
+        const int v = lane < z.topk ? z.output_index[static_cast<int64_t>(t) * z.topk + lane] : -1;
+        if (__ballot(v >= 0) != 0) continue;
+        i32x4* row = reinterpret_cast<i32x4*>(z.y + static_cast<int64_t>(t) * z.hidden);
+        for (int i = lane; i < nvec; i += kWave) __builtin_nontemporal_store(i32x4{0, 0, 0, 0}, row + i);
+      }
+    }
+  }
   if (dynamic && threadIdx.x == 0) {  // every claim of this workgroup is done: count it out
     if (atomicAdd(&g.sched[8], 1) == static_cast<int>(gridDim.x) - 1) {
       for (int r = 0; r < 8; ++r) atomicExch(&g.sched[r], 0);

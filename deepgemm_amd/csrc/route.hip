@@ -137,8 +137,9 @@ __device__ __forceinline__ void zero_sched(const RouteArgs& a) {
 }
 
 __global__ __launch_bounds__(kSmallThreads) void route_small_kernel(RouteArgs a) {
+  zero_sched(a);  // (also when GEMM1 routes: the WIDE GEMM1 then returns at once, and the
+                  // combine reads its zero-fill claim counter as zero)
   if (route_skipped(a)) return;
-  zero_sched(a);
   __shared__ int s_cnt[kSmallWaves][kSmallMaxExperts];
   __shared__ int s_tot[kSmallMaxExperts];
   __shared__ int s_off[kSmallMaxExperts + 1];
@@ -186,8 +187,8 @@ __device__ __forceinline__ WaveRange chunk_wave_range(int64_t ntasks, int chunk,
 // writes the chunk's totals and, when wave_counts is given, the per-wave rows.
 __global__ __launch_bounds__(kChunkThreads) void route_count_kernel(RouteArgs a, int chunk_tasks) {
   __shared__ int s_cnt[kChunkWaves][kMaxExperts];
-  if (route_skipped(a)) return;
   zero_sched(a);
+  if (route_skipped(a)) return;
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int E = a.num_experts;
