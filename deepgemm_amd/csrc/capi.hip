@@ -373,6 +373,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   if (zero_fill) {
     g1.zf.y = static_cast<uint16_t*>(a->y);
     g1.zf.claim = zfill_claim;
+    g1.zf.idle = zfill_claim + 1;
     g1.zf.output_index = at<int32_t>(ws, l.output_index_offset);
     g1.zf.runtime_tokens = a->runtime_num_tokens;
     g1.zf.host_tokens = a->num_tokens;
@@ -382,7 +383,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
 
   mmoe::GemmArgs g2 = g1;
   memset(&g2.sw, 0, sizeof(g2.sw));
-  memset(&g2.zf, 0, sizeof(g2.zf));
+  if (zero_fill) g2.zf.idle = zfill_claim + 2;  // (the same chunks, claimed on from GEMM1's)
   g2.route_in_kernel = 0;
   g2.a = at<uint8_t>(ws, l.act_offset);
   g2.row_token = nullptr;

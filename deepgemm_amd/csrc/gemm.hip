@@ -1729,10 +1729,10 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
     }
     __syncthreads();
   }
-  if (kSwiglu && g.zf.y != nullptr && !dynamic) {
+  if (g.zf.y != nullptr && !dynamic) {
     // out of tiles: the zero y rows of tokens without a valid routed slot, a claimed chunk of
     // kZeroFillTokens tokens at a time (a wave a token), while other workgroups still run tiles
-    // (claim[1] counts the workgroups out of tiles); the combine writes the chunks left. Only
+    // (z.idle counts the workgroups out of tiles); the combine writes the chunks left. Only
     // with the static deal (many tiles a workgroup): with claimed tiles the idle end is short,
     // and the zero rows' writes slowed the last tiles by more than the combine saved (c2: +28 us
     // per layer; c3: -60 us).
@@ -1741,11 +1741,11 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
     const int nchunks = (tokens + kZeroFillTokens - 1) / kZeroFillTokens;
     const int lane = lane_id(), wave = static_cast<int>(threadIdx.x) / kWave;
     const int nvec = z.hidden >> 3;
-    if (threadIdx.x == 0) atomicAdd(z.claim + 1, 1);
+    if (threadIdx.x == 0) atomicAdd(z.idle, 1);
     for (;;) {
       __syncthreads();  // every thread has read s_item
       if (threadIdx.x == 0) {
-        const int idle = __hip_atomic_load(z.claim + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int idle = __hip_atomic_load(z.idle, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_item = idle >= static_cast<int>(gridDim.x) ? nchunks : atomicAdd(z.claim, 1);
       }
       __syncthreads();

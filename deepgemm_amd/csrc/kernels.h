@@ -62,15 +62,17 @@ struct SwigluEpilogue {
   float clamp;
 };
 
-// WIDE GEMM1 (ZeroFill::y set): the y rows of tokens without a valid routed slot are zeros, and
+// WIDE GEMMs (ZeroFill::y set): the y rows of tokens without a valid routed slot are zeros, and
 // a workgroup that has run out of tiles writes them while others still run tiles (the kernel's
-// end leaves workgroups idle), kZeroFillTokens tokens at a time claimed from claim[0]; claim[1]
-// counts the workgroups out of tiles. The routing launch of the same call zeroes both. The
-// combine then skips those tokens in the chunks claimed (CombineArgs::zfill_claim). y null: off.
+// end leaves workgroups idle), kZeroFillTokens tokens at a time claimed from *claim (GEMM1
+// first, GEMM2 goes on from where it stopped); *idle counts the kernel's workgroups out of
+// tiles. The routing launch of the same call zeroes the counters. The combine then skips those
+// tokens in the chunks claimed (CombineArgs::zfill_claim). y null: off.
 constexpr int kZeroFillTokens = 64;
 struct ZeroFill {
   uint16_t* y;                  // bf16 [S, hidden]
-  int32_t* claim;               // [2]
+  int32_t* claim;
+  int32_t* idle;
   const int32_t* output_index;  // [S, topk]
   const int32_t* runtime_tokens;
   int host_tokens, topk, hidden;
@@ -103,7 +105,7 @@ struct GemmArgs {
   // WIDE kernel work claiming (kSchedInts ints, zero at launch; the kernel leaves them zero):
   // [0..7] per-XCD claim counters, [8] finished workgroups. Null: static dealing.
   int32_t* sched;
-  ZeroFill zf;  // WIDE GEMM1 only
+  ZeroFill zf;  // WIDE kernels only
   // Set by launch_grouped_gemm for a row bound that selects the WIDE kernel while the actual rows
   // are only known on the device (graph replays): the 8-wave and the WIDE kernel are both
   // launched, and each returns at once unless the routed rows (*dual_rows, the routing's
@@ -116,7 +118,7 @@ struct GemmArgs {
   float* row_pmax;
 };
 constexpr int kSchedInts = 16;
-constexpr int kZeroFillClaim = 9;  // GEMM1's sched ints 9 and 10: ZeroFill::claim
+constexpr int kZeroFillClaim = 9;  // GEMM1's sched int 9: ZeroFill::claim; 10, 11: the GEMMs' idle
 
 // Grouped FP8 GEMM over expert-contiguous rows: c[r, n] = bf16((sum_k a[r,k] b[e,n,k]) *
 // a_scale[r] * b_scale[e,n]). Persistent: the grid strides over the tiles, enumerated on the

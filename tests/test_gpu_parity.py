@@ -529,8 +529,8 @@ def test_wide_claim_counters_return_to_zero(mm, cuda):
     """The WIDE GEMMs claim items from per-XCD counters in route_scratch when a workgroup has few
     items; the last workgroup of each GEMM resets them, so after a call (and after a GEMM2 run on
     its own) they read zero again, and a second call on the same scratch is bitwise identical.
-    GEMM1's zero-fill counters (sched[0, 9:11]: chunks of 64 tokens whose zero rows its idle
-    workgroups wrote, and the workgroups out of tiles) are the exception: the combine reads
+    The zero-fill counters (sched[0, 9:12]: chunks of 64 tokens whose zero rows idle WIDE
+    workgroups wrote, and each GEMM's workgroups out of tiles) are the exception: the combine reads
     them, and the next call's routing launch zeroes them."""
     s, e, hdim, inter, k = 2048, 4, 512, 256, 6
     x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=31, global_experts=8)
@@ -541,12 +541,12 @@ def test_wide_claim_counters_return_to_zero(mm, cuda):
     torch.cuda.synchronize()
     assert buf.scratch_view("meta")[1].item() == 1, "the WIDE GEMM1 ran"
     sched = buf.scratch_view("sched").cpu()  # [GEMM1, GEMM2] x 16
-    sched[0, 9:11] = 0
+    sched[0, 9:12] = 0
     assert torch.all(sched == 0)
     mm.LayerCall(torch.empty_like(y1), l1, l2, buf).run(3, 3)  # GEMM2 alone
     torch.cuda.synchronize()
     sched = buf.scratch_view("sched").cpu()
-    sched[0, 9:11] = 0
+    sched[0, 9:12] = 0
     assert torch.all(sched == 0)
     y2 = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
     torch.cuda.synchronize()
