@@ -712,6 +712,44 @@ def test_graph_full_shape_both_kernels(mm, cuda, full_weights):
         assert torch.all(y[n:] == 7.0)
 
 
+def test_graph_ep_share_zero_rows(mm, cuda, full_weights):
+    """An EP share (256 global experts, ~45% of the tokens without a local slot) in a
+    12288-token bucket: a full replay runs the WIDE kernels, whose idle workgroups write the
+    zero rows of the live tokens without a slot (the combine skips the chunks they claimed), a
+    short one the 8-wave kernels. Every replay is bitwise equal to an eager call on the same
+    prefix (zero rows included: y starts at 7.0), and rows past it are left alone."""
+    l1, l2 = full_weights[0], full_weights[1]
+    s_max = 12288
+    x_fp8, x_sf, idx, w = make_tokens(s_max, 4096, 32, 6, seed=444, global_experts=256)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    for t, src in ((buf.x, x_fp8), (buf.x_sf, x_sf), (buf.topk_idx, idx), (buf.topk_weights, w)):
+        t[:s_max].copy_(src)
+    y = torch.zeros((s_max, 4096), dtype=torch.bfloat16, device=cuda)
+    log("EP-share graph: warm-up and capture at 12288 tokens")
+    mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
+    ref_buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    for n, wide in ((s_max, True), (1024, False), (s_max - 77, True)):
+        log(f"  replay with runtime tokens={n}")
+        y.fill_(7.0)
+        buf.cuda_graph_num_tokens.fill_(n)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert bool(buf.scratch_view("meta")[1].item() == 1) == wide, f"n={n}: kernel choice"
+        y_ref = torch.full((n, 4096), 7.0, dtype=torch.bfloat16, device=cuda)
+        run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2, y=y_ref)
+        torch.cuda.synchronize()
+        unrouted = (idx[:n] < 0) | (idx[:n] >= 32)
+        zero_rows = unrouted.all(dim=1).to(cuda)
+        assert int(zero_rows.sum()) > n // 3, "many tokens without a local slot"
+        assert torch.all(y_ref[zero_rows] == 0)
+        assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
+        assert torch.all(y[n:] == 7.0)
+
+
 # ------------------------------------------------------------------ pre/post-process
 @pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
 def test_deepep_pre_post_process(mm, cuda, ids_dtype):
