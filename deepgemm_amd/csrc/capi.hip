@@ -46,9 +46,14 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   memset(l, 0, sizeof(*l));
   l->row_capacity = rows;
   l->num_chunks = chunks;
+  // The decode pipeline's counters and meta come first, at offsets that no shape changes: the
+  // counters must read zero when a call starts and every call leaves them zero, so a scratch
+  // reused across shapes (or the static one) never hands a call another section's bytes as
+  // counters; meta[3] (the status) sits where mmoe_scratch_status finds it without the shape.
+  l->pipe_offset = take(mmoe::kPipeInts * 4);
+  l->meta_offset = take(16 * 4);
   l->counts_offset = take(e_local * 4);
   l->offsets_offset = take((e_local + 1) * 4);
-  l->meta_offset = take(16 * 4);
   l->chunk_counts_offset = take(mmoe::route_count_ints(tasks, static_cast<int>(e_local)) * 4);
   l->output_index_offset = take((tasks > 0 ? tasks : 1) * 4);
   l->row_token_offset = take(rows * 4);
@@ -61,7 +66,6 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
   l->row_dest_offset = take(rows * 4);
   l->sched_offset = take(2 * mmoe::kSchedInts * 4);
-  l->pipe_offset = take(mmoe::kPipeInts * 4);
   l->pmax_offset = take(std::min<int64_t>(rows, mmoe::gemm_route_max_tasks()) *
                         (2 * static_cast<int64_t>(intermediate) / 64) * 4);
   l->total_bytes = off;
@@ -124,6 +128,7 @@ int validate_forward(const mmoe_forward_args* a) {
     return MMOE_ERR_UNSUPPORTED_SHAPE;
   if (a->schedule < MMOE_SCHEDULE_AUTO || a->schedule > MMOE_SCHEDULE_STAGED)
     return MMOE_ERR_SCHEDULE;
+  if ((a->debug_flags & ~MMOE_DEBUG_NO_WAIT) != 0) return MMOE_ERR_ARGUMENT;
   mmoe_symm_layout sl;
   plan_symm(a->num_max_tokens, a->num_topk, a->hidden, &sl);
   if (a->sym_buffer_bytes >= 0 && a->sym_buffer_bytes < sl.total_bytes)
@@ -432,6 +437,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     p.meta = at<int32_t>(ws, l.meta_offset);
     p.direct_flag = direct_flag;
     p.pipe = at<int32_t>(ws, l.pipe_offset);
+    p.spin_limit = (a->debug_flags & MMOE_DEBUG_NO_WAIT) != 0 ? 0 : mmoe::kPipeSpinLimit;
     if (runs(MMOE_STAGE_COMBINE) && a->hidden % 8 == 0 && a->hidden <= mmoe::kPipeCombineMaxHidden) {
       p.y = static_cast<uint16_t*>(a->y);
       combined = true;
@@ -481,6 +487,24 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
 }
 
 static_assert(MMOE_PIPE_INTS == mmoe::kPipeInts, "the header's pipeline counter count");
+static_assert(MMOE_PIPE_INTS * 4 % 256 == 0 && MMOE_SCRATCH_STATUS_OFFSET == MMOE_PIPE_INTS * 4 + 12,
+              "meta follows the pipeline counters directly (the status offset of every layout)");
+
+int mmoe_scratch_status(const void* route_scratch, int32_t* out, void* stream) {
+  if (out == nullptr) return MMOE_ERR_NULL_POINTER;
+  const void* base = route_scratch;
+  if (base == nullptr) {  // the static scratch of mmoe_forward_static on this device
+    void* p = nullptr;
+    const int st = static_scratch_address(&p);
+    if (st != MMOE_OK) return st;
+    base = p;
+  }
+  const void* src = static_cast<const uint8_t*>(base) + MMOE_SCRATCH_STATUS_OFFSET;
+  return hipMemcpyAsync(out, src, sizeof(int32_t), hipMemcpyDefault,
+                        static_cast<hipStream_t>(stream)) == hipSuccess
+             ? MMOE_OK
+             : MMOE_ERR_HIP;
+}
 
 int mmoe_forward(const mmoe_forward_args* a, void* stream) {
   return mmoe_forward_stages(a, MMOE_STAGE_ROUTE, MMOE_STAGE_COMBINE, stream);

@@ -1173,7 +1173,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
         ra.counts[e] = s_count[e];
         if (ra.stats != nullptr) ra.stats[e] += s_count[e];
       }
-      if (threadIdx.x == 0) ra.meta[0] = s_off[E] < ra.row_cap ? s_off[E] : static_cast<int>(ra.row_cap);
+      if (threadIdx.x == 0) {
+        ra.meta[0] = s_off[E] < ra.row_cap ? s_off[E] : static_cast<int>(ra.row_cap);
+        ra.meta[3] = 0;  // the call's status: no bounded wait on this path
+      }
     }
   } else {
     for (int e = threadIdx.x; e <= E; e += kGemmThreads) {
@@ -1257,7 +1260,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 // requant kernel's arithmetic, so the same bits; the group's first GEMM2 item also writes act
 // and amax out). Every GEMM1 item is claimed before any GEMM2 item of its XCD, and a GEMM1 item
 // waits on nothing, so every wait ends; a wait is also bounded (kPipeSpinLimit polls), and one
-// that runs out counts in meta[3] instead of hanging. The workgroup that finishes last runs the
+// that runs out is counted (the launch's last workgroup leaves the count in meta[3], the call's
+// status) instead of hanging. The workgroup that finishes last runs the
 // queue of any XCD that no workgroup ran (none when the launch covers the chip), alone and
 // start to end.
 //
@@ -1270,8 +1274,6 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 // device-coherent loads. Every GEMM2 item is claimed by a workgroup of its XCD, or by the last
 // workgroup for an XCD without any, so every wait ends. The workgroup that leaves last sets the
 // counters back to zero.
-constexpr int kPipeSpinLimit = 1 << 20;  // polls of a group count (far longer than any item)
-
 __device__ __forceinline__ int hw_xcc_id() {
   int v;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
@@ -1284,9 +1286,10 @@ __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" :
 // Later loads of this CU miss its L1 (they read the XCD's L2, where the producer's stores are).
 __device__ __forceinline__ void l1_invalidate() { asm volatile("buffer_inv sc0" ::: "memory"); }
 
-// Thread-level poll (a vector atomic load: lane-divergent code) until *c >= target.
-__device__ __forceinline__ bool wait_count(const int32_t* c, int target) {
-  for (int i = 0; i < kPipeSpinLimit; ++i) {
+// Thread-level poll (a vector atomic load: lane-divergent code) until *c >= target, at most
+// `limit` polls (false: it ran out).
+__device__ __forceinline__ bool wait_count(const int32_t* c, int target, int limit) {
+  for (int i = 0; i < limit; ++i) {
     if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) return true;
     __builtin_amdgcn_s_sleep(2);
   }
@@ -1319,10 +1322,12 @@ __device__ void pipe_combine_token(const PipeArgs& p, int64_t t, const uint8_t* 
     const int ev = s_ev[task];
     if (ev != 255) {
       bool ok = true;
-      for (int grp = s_gprefix[ev]; grp < s_gprefix[ev + 1]; ++grp) ok = ok && wait_count(&done1[grp], n1);
+      for (int grp = s_gprefix[ev]; grp < s_gprefix[ev + 1]; ++grp)
+        ok = ok && wait_count(&done1[grp], n1, p.spin_limit);
       row = __hip_atomic_load(&ra.output_index[task], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = ok && wait_count(&done2[ev * kPipeDone2Stride], n2 * (s_gprefix[ev + 1] - s_gprefix[ev]));
-      if (!ok) atomicAdd(&p.meta[3], 1);
+      ok = ok && wait_count(&done2[ev * kPipeDone2Stride], n2 * (s_gprefix[ev + 1] - s_gprefix[ev]),
+                            p.spin_limit);
+      if (!ok) atomicAdd(&p.pipe[kPipeFailAt], 1);
     }
   }
   float sum[V][8];
@@ -1526,14 +1531,13 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
     if (threadIdx.x == 0) {
       ra.meta[0] = s_off[E] < ra.row_cap ? s_off[E] : static_cast<int>(ra.row_cap);
       p.meta[1] = 0;  // the requant read GEMM1's y
-      p.meta[3] = 0;  // bounded waits that ran out (none can have by now)
       if (p.direct_flag != nullptr) *p.direct_flag = 0;
-      if (hw >= kPipeXcds) atomicAdd(&p.meta[3], 1);  // an XCD id this launch does not expect
+      if (hw >= kPipeXcds) atomicAdd(&p.pipe[kPipeFailAt], 1);  // an XCD id this launch does not expect
     }
   }
   // more groups than counters (the host's task bound rules it out): flagged, and no items
   const bool too_many = s_gprefix[E] > kMaxPipeGroups;
-  if (too_many && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&p.meta[3], 1);
+  if (too_many && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&p.pipe[kPipeFailAt], 1);
   const int G = too_many ? 0 : s_gprefix[E];
   const int n1 = stream_blocks(g1), n2 = stream_blocks(g2);
   const float* task_w = reinterpret_cast<const float*>(smem);  // valid until the first item's loads
@@ -1602,7 +1606,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
     } else {
       // the weights go out first; then the group's rows, requantized from y into LDS
       const auto stage_rows = [&]() {
-        if (threadIdx.x == 0 && !wait_count(&done1[grp], n1)) atomicAdd(&p.meta[3], 1);
+        if (threadIdx.x == 0 && !wait_count(&done1[grp], n1, p.spin_limit)) atomicAdd(&p.pipe[kPipeFailAt], 1);
         __syncthreads();
         l1_invalidate();
         if (mrows > 32) stage_rows_from_y<2>(p, row0, mrows, nb == 0, smem, s_inv, s_tt.xs);
@@ -1634,10 +1638,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
       pipe_combine_token(p, t, s_ev, s_gprefix, n1, n2, done1, done2, part);
   }
   // the workgroup that leaves last (every other one has made its last counter access): the
-  // counters back to zero for the next launch
+  // count of waits that ran out into meta[3] (the call's status), the counters back to zero
+  // for the next launch. Each wave's counter atomics are complete (vmcnt) before its
+  // workgroup counts itself out, so the last one reads every failure.
+  vm_drain();
   __syncthreads();
-  if (threadIdx.x == 0)
-    s_word = atomicAdd(p.pipe + kPipeExitAt, 1) == static_cast<int>(gridDim.x) - 1 ? 1 : 0;
+  if (threadIdx.x == 0) {
+    const bool last = atomicAdd(p.pipe + kPipeExitAt, 1) == static_cast<int>(gridDim.x) - 1;
+    if (last) p.meta[3] = __hip_atomic_load(p.pipe + kPipeFailAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_word = last ? 1 : 0;
+  }
   __syncthreads();
   if (s_word != 0) {
     for (int i = threadIdx.x; i < kPipeHeader + G; i += kGemmThreads) p.pipe[i] = 0;

@@ -200,13 +200,20 @@ hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream)
 // pipe: kPipeInts counters, zero when the launch starts (its last workgroup to leave zeroes
 // them again), each header counter in a 128-byte line of its own (every workgroup goes to them
 // at about the same time): the per-XCD claim counters at x * kPipeLine, the count of workgroups
-// that ran out of items at kPipeFinishAt, the count of workgroups that left at kPipeExitAt;
-// then GEMM1 items done per group ([kPipeDone1At..], kMaxPipeGroups) and GEMM2 items done per
-// expert (expert e's at kPipeDone2At + e * kPipeDone2Stride: the combine's waves poll them).
+// that ran out of items at kPipeFinishAt, the count of workgroups that left at kPipeExitAt
+// (the count of bounded waits that ran out next to it, at kPipeFailAt: rarely touched; the last
+// workgroup to leave copies it to meta[3]); then GEMM1 items done per group ([kPipeDone1At..],
+// kMaxPipeGroups) and GEMM2 items done per expert (expert e's at kPipeDone2At + e *
+// kPipeDone2Stride: the combine's waves poll them).
 constexpr int kPipeXcds = 8;
 constexpr int kPipeLine = 32;
 constexpr int kPipeFinishAt = kPipeXcds * kPipeLine;
 constexpr int kPipeExitAt = (kPipeXcds + 1) * kPipeLine;
+constexpr int kPipeFailAt = kPipeExitAt + 1;
+// Polls of a bounded wait (a group's or an expert's count; far longer than any item). A wait
+// that runs out counts itself and goes on, so the launch always ends; the call's status
+// (meta[3], mmoe_scratch_status) then reports that its output is not valid.
+constexpr int kPipeSpinLimit = 1 << 20;
 constexpr int kPipeHeader = (kPipeXcds + 2) * kPipeLine;
 constexpr int kMaxPipeGroups = 512;  // groups of <= 64 rows: S*K <= 8192 rows over <= 255 experts
 constexpr int kMaxPipeExperts = 256;
@@ -221,10 +228,13 @@ struct PipeArgs {
   float* act_scale;      // [rows]
   float* amax;           // [rows] (with act)
   int32_t* meta;         // [1] = 0 (the requant read y); [3] = bounded waits that ran out
+                         // (written at the end of the launch)
   int32_t* direct_flag;  // set to 0 (no direct rows), or null
   int32_t* pipe;
   uint16_t* y;           // non-null: the launch also runs the combine into y (bf16 [S, H];
                          // H % 8 == 0 and H <= kPipeCombineMaxHidden)
+  int spin_limit;        // polls of a bounded wait: kPipeSpinLimit, or 0 to test the error path
+                         // (every wait then gives up at once)
 };
 constexpr int kPipeCombineMaxHidden = 64 * 8 * 8;  // one wave a token: 8 16-byte groups a lane
 bool decode_pipeline_supported(const GemmArgs& g1, const GemmArgs& g2, int num_cus);

@@ -110,6 +110,7 @@ __device__ void publish_offsets(const RouteArgs& a, const int* s_tot, int* s_off
       s_off[a.num_experts] = carry;
       if (writer) {
         a.meta[0] = static_cast<int32_t>(routed < a.row_cap ? routed : a.row_cap);
+        a.meta[3] = 0;  // the call's status: the staged kernels have no bounded waits
         a.meta[4] = largest;
       }
     }

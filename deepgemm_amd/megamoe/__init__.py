@@ -513,8 +513,38 @@ def _forward_args(y, l1_weights, l2_weights, stats, sym_buffer, activation_clamp
         num_tokens=y.size(0), num_max_tokens=sym_buffer.num_max_tokens_per_rank,
         num_experts=sym_buffer.num_experts, num_topk=sym_buffer.num_topk,
         hidden=sym_buffer.hidden, intermediate=sym_buffer.intermediate_hidden,
-        activation_clamp=clamp, schedule=schedule, reserved=0)
+        activation_clamp=clamp, schedule=schedule, debug_flags=0)
     return args
+
+
+_DEBUG_CHECK_ENV = "MEGAMOE_DEBUG_CHECK"
+
+
+def last_call_status(sym_buffer: SymmBuffer) -> int:
+    """Status of the last layer call on ``sym_buffer`` (synchronises the current stream): 0 when
+    its output is valid, else the number of bounded waits of the one-launch decode pipeline that
+    ran out (``mmoe_scratch_status``). Such a wait only runs out when other work holds the GPU's
+    CUs far longer than any of the layer's own items; the layer then still ends, but ``y`` is not
+    valid."""
+    out = torch.empty((1,), dtype=torch.int32, device=sym_buffer.route_scratch.device)
+    _capi.check(_capi.load().mmoe_scratch_status(sym_buffer.route_scratch.data_ptr(),
+                                                 ctypes.cast(out.data_ptr(),
+                                                             ctypes.POINTER(ctypes.c_int32)),
+                                                 _stream_handle()), "last_call_status")
+    return int(out.item())
+
+
+def _check_status(sym_buffer: SymmBuffer) -> None:
+    """MEGAMOE_DEBUG_CHECK=1: after an eager call, synchronise and raise RuntimeError when the
+    call's status reports bounded waits that ran out (off by default: it costs a host sync)."""
+    if os.getenv(_DEBUG_CHECK_ENV, "0").strip().lower() not in ("1", "true", "yes", "on"):
+        return
+    if _is_current_stream_capturing():
+        return
+    failed = last_call_status(sym_buffer)
+    if failed != 0:
+        raise RuntimeError(f"DCU MegaMoE decode pipeline: {failed} bounded waits ran out (the "
+                           "GPU's CUs were held by other work); the layer output is not valid")
 
 
 def _launch_layer(y, l1_weights, l2_weights, stats, sym_buffer, activation_clamp, schedule,
@@ -523,6 +553,8 @@ def _launch_layer(y, l1_weights, l2_weights, stats, sym_buffer, activation_clamp
                          runtime_num_tokens)
     fn = getattr(_capi.load(), entry)
     _capi.check(fn(ctypes.byref(args), _stream_handle()), "fp8_mega_moe")
+    if entry == "mmoe_forward":
+        _check_status(sym_buffer)
 
 
 class LayerCall:
@@ -658,6 +690,7 @@ __all__ = [
     "deepep_deepgemm_postprocess_channelwise",
     "fp8_mega_moe",
     "fp8_w8a8_mega_moe",
+    "last_call_status",
 ]
 
 __version__ = "0.1"

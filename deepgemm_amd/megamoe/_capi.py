@@ -16,6 +16,8 @@ MMOE_OK = 0
 MMOE_ERR_STATIC_SCRATCH = -15
 MMOE_STATIC_SCRATCH_BYTES = 128 << 20
 MMOE_PIPE_INTS = 4928
+MMOE_SCRATCH_STATUS_OFFSET = MMOE_PIPE_INTS * 4 + 3 * 4
+MMOE_DEBUG_NO_WAIT = 1
 MMOE_SCHEDULE_AUTO = 0
 MMOE_SCHEDULE_PERSISTENT = 1
 MMOE_SCHEDULE_STAGED = 2
@@ -85,7 +87,7 @@ class ForwardArgs(ctypes.Structure):
         ("intermediate", c_i32),
         ("activation_clamp", ctypes.c_float),
         ("schedule", c_i32),
-        ("reserved", c_i32),
+        ("debug_flags", c_i32),
     ]
 
 
@@ -100,6 +102,7 @@ SIGNATURES = {
     "mmoe_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "mmoe_forward": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
     "mmoe_forward_static": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
+    "mmoe_scratch_status": (ctypes.c_int, [c_p, ctypes.POINTER(c_i32), c_p]),
     "mmoe_route": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
     "mmoe_forward_stages": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), ctypes.c_int,
                                            ctypes.c_int, c_p]),

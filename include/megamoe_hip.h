@@ -82,6 +82,8 @@ typedef struct mmoe_scratch_layout {
   int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R; [1] = 1: GEMM1 left
                                   the bf16 pre-activation h in y's bytes; [2] = 1: GEMM2 wrote
                                   the rows of single-slot tokens straight to y (row_dest);
+                                  [3] = the call's status (bounded waits of the decode pipeline
+                                  that ran out; 0 = y is valid; MMOE_SCRATCH_STATUS_OFFSET);
                                   [4] = the largest expert's row count (routing launches) */
   int64_t chunk_counts_offset; /* int32 [num_chunks, E] per-chunk counts, then
                                   [num_chunks, 16, E] per-wave counts (routing) */
@@ -102,14 +104,25 @@ typedef struct mmoe_scratch_layout {
                                   (GEMM1, GEMM2): zeroed by the routing stage, left at zero by
                                   the GEMMs themselves */
   int64_t pipe_offset;         /* int32 [MMOE_PIPE_INTS] counters of the one-launch decode
-                                  pipeline (GEMM1 + requant + GEMM2 + combine): zero when the scratch is
-                                  new (allocate it zero-filled), and left zero by every call */
+                                  pipeline (GEMM1 + requant + GEMM2 + combine), always at offset
+                                  0 whatever the shape: they must be zero when a call starts --
+                                  zero when the scratch is new (allocate it zero-filled), and
+                                  left zero by every call, so a scratch may serve calls of any
+                                  shape in turn */
   int64_t pmax_offset;         /* f32   [min(rows, 8192), 2I/64] the decode pipeline's per-row
                                   max |y| of each 64-column block of GEMM1's output */
 } mmoe_scratch_layout;
 
 #define MMOE_ROUTE_CHUNK 1024
 #define MMOE_PIPE_INTS 4928
+/* Byte offset of meta[3] (the status of the last call) in every route_scratch: the pipeline
+ * counters (MMOE_PIPE_INTS ints at offset 0) and then meta. */
+#define MMOE_SCRATCH_STATUS_OFFSET (MMOE_PIPE_INTS * 4 + 3 * 4)
+
+/* Bits of mmoe_forward_args.debug_flags (0 in production). */
+#define MMOE_DEBUG_NO_WAIT 1 /* every bounded wait of the decode pipeline gives up at its first
+                                poll: the launch still ends, and the call's status reports the
+                                waits (tests of the error path) */
 
 /* Arguments of one layer call. Replaces the argument list of fp8_mega_moe_impl,
  * csrc/apis/mega_dcu.hpp:338-354, and of
@@ -137,7 +150,7 @@ typedef struct mmoe_forward_args {
   int32_t intermediate;              /* I */
   float activation_clamp;            /* +inf = no clamp (reference: activation_clamp=None) */
   int32_t schedule;                  /* MMOE_SCHEDULE_* */
-  int32_t reserved;                  /* must be 0 */
+  int32_t debug_flags;               /* 0, or MMOE_DEBUG_* bits (tests only) */
 } mmoe_forward_args;
 
 /* get_token_alignment_for_mega_moe, csrc/apis/mega_dcu.hpp:24-26 (kTokenAlignment,
@@ -165,8 +178,27 @@ const char* mmoe_status_string(int status);
 /* The layer: fp8_mega_moe / fp8_mega_moe_with_graph_tokens,
  * csrc/apis/mega_dcu.hpp:338-518 -> csrc/kernels/mega_moe_fused_hip.cu:72-121 and the staged
  * path megamoe/large_opt.py:367-508. Routing -> GEMM1 with fused SwiGLU -> requant -> GEMM2
- * -> combine. */
+ * -> combine.
+ * Precondition: the first MMOE_PIPE_INTS * 4 bytes of route_scratch are zero when the call
+ * starts. Allocate route_scratch zero-filled once; every call leaves those bytes zero again
+ * (whatever its shape), so nothing needs clearing between calls. Calls that overlap on one
+ * route_scratch race.
+ * The return code covers validation and launch errors only. At decode sizes (S*K <= 8192 on
+ * the 256-CU MI355X) the layer is one persistent launch whose workgroups hand rows to each other
+ * through bounded waits: it needs the whole GPU, and a wait that runs out (another kernel
+ * holding CUs for longer than the bound) leaves a wrong y. The launch still ends, and the call's
+ * status (mmoe_scratch_status) is nonzero then. */
 int mmoe_forward(const mmoe_forward_args* args, void* stream);
+
+/* Status of the last mmoe_forward / mmoe_forward_static call on route_scratch (NULL: the static
+ * scratch of the current device): enqueues on `stream` a 4-byte copy of it to *out (device
+ * memory, or pinned host memory read after the stream has reached this point). 0: that call's
+ * y is valid; > 0: the number of bounded waits of its decode pipeline that ran out (y is not
+ * valid). No counterpart in the reference, whose persistent kernel waits for its L2 queue
+ * without a bound (deep_gemm/include/deep_gemm/scheduler/mega_moe_dcu.cuh:52-53) and aborts the
+ * kernel when a barrier times out (deep_gemm/include/deep_gemm/comm/mega_moe_dcu.cuh:76-90,
+ * :104-113); it is for callers that must detect a wait that ran out. */
+int mmoe_scratch_status(const void* route_scratch, int32_t* out, void* stream);
 
 /* Allocation-free variant of mmoe_forward. No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops,

@@ -96,13 +96,44 @@ def test_layouts():
     assert lib.mmoe_route_scratch_layout(1, 32, 384, 6, 4096, 2048, ctypes.byref(lay)) == 0
     assert lay.total_bytes == nb.value
     assert lay.row_capacity >= 384 * 6
-    offs = [lay.counts_offset, lay.offsets_offset, lay.meta_offset, lay.chunk_counts_offset,
-            lay.output_index_offset, lay.row_token_offset, lay.row_weight_offset,
-            lay.m_indices_offset, lay.act_scale_offset, lay.amax_offset,
-            lay.y_offset, lay.act_offset,
-            lay.part_offset]
+    offs = [lay.pipe_offset, lay.meta_offset, lay.counts_offset, lay.offsets_offset,
+            lay.chunk_counts_offset, lay.output_index_offset, lay.row_token_offset,
+            lay.row_weight_offset, lay.m_indices_offset, lay.act_scale_offset, lay.amax_offset,
+            lay.y_offset, lay.act_offset, lay.part_offset, lay.row_dest_offset, lay.sched_offset,
+            lay.pmax_offset]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert lay.part_offset + lay.row_capacity * 4096 * 2 <= lay.total_bytes
+
+
+@pytest.mark.parametrize("shape", [
+    (1, 32, 384, 6, 4096, 2048), (1, 32, 1152, 6, 4096, 2048), (1, 32, 200, 6, 4096, 2048),
+    (1, 4, 16, 3, 256, 128), (1, 255, 300, 6, 256, 128), (1, 64, 2000, 6, 512, 256),
+    (1, 1024, 8, 16, 128, 128), (1, 32, 0, 6, 4096, 2048),
+])
+def test_pipe_counters_and_status_sit_at_fixed_offsets(shape):
+    """The decode pipeline's counters (which must read zero when a call starts; each call leaves
+    them zero) are at offset 0 in every layout, and meta right after them, so one scratch can
+    serve calls of any shape in turn without handing a call another section's bytes as its
+    counters, and the status word is found without the shape."""
+    lib = _capi.load()
+    lay = _capi.ScratchLayout()
+    assert lib.mmoe_route_scratch_layout(*shape, ctypes.byref(lay)) == 0
+    assert lay.pipe_offset == 0
+    assert lay.meta_offset == _capi.MMOE_PIPE_INTS * 4
+    assert lay.meta_offset + 3 * 4 == _capi.MMOE_SCRATCH_STATUS_OFFSET
+    others = [getattr(lay, f) for f, _ in _capi.ScratchLayout._fields_
+              if f.endswith("_offset") and f not in ("pipe_offset", "meta_offset")]
+    assert min(others) >= lay.meta_offset + 16 * 4
+
+
+def test_scratch_status_rejects_null_output():
+    lib = _capi.load()
+    assert lib.mmoe_scratch_status(None, None, None) == -1
+
+
+def test_debug_flags_are_validated():
+    lib = _capi.load()
+    assert lib.mmoe_forward(ctypes.byref(_args(debug_flags=2)), None) == -14
 
 
 @pytest.mark.parametrize("args,code", [
@@ -121,7 +152,7 @@ def test_layout_validation_codes(args, code):
 
 def _args(**kw):
     base = dict(num_tokens=4, num_max_tokens=384, num_experts=32, num_topk=6, hidden=4096,
-                intermediate=2048, activation_clamp=math.inf, schedule=0, reserved=0,
+                intermediate=2048, activation_clamp=math.inf, schedule=0, debug_flags=0,
                 route_scratch_bytes=1 << 40, sym_buffer_bytes=1 << 40)
     base.update(kw)
     a = _capi.ForwardArgs()

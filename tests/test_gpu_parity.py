@@ -627,52 +627,88 @@ def test_layer_no_routed_rows(mm, cuda):
 
 
 # ------------------------------------------------------------------ graph-bucket mode
-@pytest.mark.parametrize("flag", ["big_fused_cuda_graph", "stages_fused_cuda_graph"])
-@pytest.mark.parametrize("bucket", [(200, 8, 16), (2048, 4, 16), (3000, 8, None), (2000, 64, None)])
-def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
-    """Capture once at the bucket size, replay with several device token counts: every replay
-    equals an eager call on that prefix (bitwise) and leaves rows past the prefix untouched.
-    The large buckets' row bound selects the 4-wave WIDE GEMMs, so both those and the 8-wave
-    kernels are captured and the routed rows choose on the device: WIDE from
-    max(8193, 256 * E) rows (the 3000-token bucket's full replays), the 8-wave kernels below
-    (short prefixes) -- the same sums in the same order either way, so the same bits. Buckets
-    of more than 8192 tasks also leave the routing to GEMM1 when the live tasks fit in it; the
-    64-expert bucket does so without selecting WIDE (fewer than 256 rows per expert)."""
-    s_max, e, g = bucket
-    hdim, inter, k = 512, 256, 6
-    x_fp8, x_sf, idx, w = make_tokens(s_max, hdim, e, k, seed=21, global_experts=g)
-    l1, l2 = make_weights_gpu(e, hdim, inter, seed=22, mm=mm)
-    buf = mm.get_symm_buffer_for_mega_moe(None, e, s_max, k, hdim, inter)
+# Every replay is checked against the oracle on its prefix (routing bit-exact, calc_diff of y),
+# as the reference checks each replayed token count against its dequantise-and-matmul baseline
+# (tests/test_mega_moe_dcu.py:563-715, comparison at :646-668), and bitwise against an eager call
+# of this library on the same prefix. Each token count is replayed twice, with the eager work and
+# host synchronisations in between, and both replays are checked.
+def _load_bucket(buf, x_fp8, x_sf, idx, w):
+    s = x_fp8.shape[0]
     for t, src in ((buf.x, x_fp8), (buf.x_sf, x_sf), (buf.topk_idx, idx), (buf.topk_weights, w)):
-        t[:s_max].copy_(src)
-    y = torch.zeros((s_max, hdim), dtype=torch.bfloat16, device=cuda)
-    log(f"graph mode {flag}: eager warm-up then capture")
-    mm.fp8_w8a8_mega_moe(y, l1, l2, buf, **{flag: True})
+        t[:s].copy_(src.to(t.device))
+
+
+def _capture_bucket(mm, y, l1, l2, buf, flag):
+    """Warm-up on a side stream, then capture one call in graph mode (the reference's order,
+    tests/test_mega_moe_dcu.py:618-631)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, **{flag: True})
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         mm.fp8_w8a8_mega_moe(y, l1, l2, buf, **{flag: True})
+    return graph
+
+
+def _oracle_prefix_check(buf, n, tr, y, unpacked=None):
+    """The replay's routing equals the oracle's on the prefix (counts, output_index) and its
+    y[:n] is within the north-star bar of the oracle's."""
+    assert np.array_equal(buf.scratch_view("counts").cpu().numpy(), tr.routing.counts), f"n={n}: counts"
+    assert np.array_equal(buf.scratch_view("output_index")[:n].cpu().numpy(),
+                          tr.routing.output_index), f"n={n}: output_index"
+    d = O.calc_diff(y[:n].cpu(), tr.y)
+    log(f"    n={n}: routed rows {tr.routing.num_rows}, calc_diff vs oracle {d:.3e}")
+    assert d <= CALC_DIFF_BAR, f"n={n}: calc_diff {d}"
+
+
+@pytest.mark.parametrize("flag", ["big_fused_cuda_graph", "stages_fused_cuda_graph"])
+@pytest.mark.parametrize("bucket", [(200, 8, 16), (2048, 4, 16), (3000, 8, None), (2000, 64, None)])
+def test_graph_capture_replay_runtime_tokens(mm, cuda, flag, bucket):
+    """Capture once at the bucket size, replay with several device token counts: every replay
+    matches the oracle on its prefix, equals an eager call on that prefix (bitwise) and leaves
+    rows past the prefix untouched. The large buckets' row bound selects the 4-wave WIDE GEMMs,
+    so both those and the 8-wave kernels are captured and the routed rows choose on the device:
+    WIDE from max(8193, 256 * E) rows (the 3000-token bucket's full replays), the 8-wave kernels
+    below (short prefixes) -- the same sums in the same order either way, so the same bits.
+    Buckets of more than 8192 tasks also leave the routing to GEMM1 when the live tasks fit in
+    it; the 64-expert bucket does so without selecting WIDE (fewer than 256 rows per expert)."""
+    s_max, e, g = bucket
+    hdim, inter, k = 512, 256, 6
+    x_fp8, x_sf, idx, w = make_tokens(s_max, hdim, e, k, seed=21, global_experts=g)
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=22, mm=mm)
+    l1c, l2c = cpu_weights(l1, l2)
+    buf = mm.get_symm_buffer_for_mega_moe(None, e, s_max, k, hdim, inter)
+    _load_bucket(buf, x_fp8, x_sf, idx, w)
+    y = torch.zeros((s_max, hdim), dtype=torch.bfloat16, device=cuda)
+    log(f"graph mode {flag} bucket={bucket}: warm-up then capture")
+    graph = _capture_bucket(mm, y, l1, l2, buf, flag)
     ref_buf = mm.SymmBuffer(None, e, s_max, k, hdim, inter)
     wide_min = max(8193, 256 * e)
     kinds = set()
     for n in (s_max, 57, 1, 0, 133, s_max - 77):
-        log(f"  replay with runtime tokens={n}")
-        y.fill_(7.0)
-        buf.cuda_graph_num_tokens.fill_(n)
-        graph.replay()
-        torch.cuda.synchronize()
-        meta = buf.scratch_view("meta").cpu()
-        live_ids = idx[:n]
-        routed = int(((live_ids >= 0) & (live_ids < e) & (w[:n] != 0)).sum())
-        assert int(meta[0].item()) == routed, f"n={n}: routed rows of this replay"
-        wide = bool(meta[1].item() == 1)
-        assert wide == (routed >= wide_min), f"n={n}: kernel choice for R={routed}"
-        kinds.add(wide)
-        if n > 0:
-            y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2)
+        tr = O.mega_moe_forward(x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1c, l2c) if n > 0 else None
+        y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2) if n > 0 else None
+        for rep in range(2):
+            log(f"  replay {rep} with runtime tokens={n}")
+            y.fill_(7.0)
+            buf.cuda_graph_num_tokens.fill_(n)
+            graph.replay()
             torch.cuda.synchronize()
-            assert torch.equal(y[:n], y_ref), f"replay n={n}"
-        assert torch.all(y[n:] == 7.0), f"rows past the prefix were written (n={n})"
+            meta = buf.scratch_view("meta").cpu()
+            live_ids = idx[:n]
+            routed = int(((live_ids >= 0) & (live_ids < e) & (w[:n] != 0)).sum())
+            assert int(meta[0].item()) == routed, f"n={n}: routed rows of this replay"
+            assert int(meta[3].item()) == 0, f"n={n}: status"
+            wide = bool(meta[1].item() == 1)
+            assert wide == (routed >= wide_min), f"n={n}: kernel choice for R={routed}"
+            kinds.add(wide)
+            if n > 0:
+                _oracle_prefix_check(buf, n, tr, y)
+                assert torch.equal(y[:n], y_ref), f"replay n={n}"
+            assert torch.all(y[n:] == 7.0), f"rows past the prefix were written (n={n})"
     if g is None:  # every slot local: the full replays run WIDE (if the rows select it) and the
         # short ones the 8-wave kernels
         assert kinds == ({True, False} if s_max * k >= wide_min else {False})
@@ -682,72 +718,232 @@ def test_graph_full_shape_both_kernels(mm, cuda, full_weights):
     """The production shape in a 2048-token bucket (every slot local: a WIDE row bound): a full
     replay runs the WIDE kernels, a short one the 8-wave kernels with GEMM1 routing in-kernel,
     also on both sides of the in-kernel routing's task limit (1365 tokens = 8190 tasks: 8-wave;
-    1366 = 8196: WIDE). Every replay is bitwise equal to an eager call on the same prefix, and
-    rows past it are left alone."""
-    l1, l2 = full_weights[0], full_weights[1]
+    1366 = 8196: WIDE). Every replay matches the oracle on its prefix, is bitwise equal to an
+    eager call on the same prefix, and leaves rows past it alone."""
+    l1, l2, l1c, l2c, unpacked = full_weights
     s_max = 2048
     x_fp8, x_sf, idx, w = make_tokens(s_max, 4096, 32, 6, seed=333, global_experts=None)
     buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
-    for t, src in ((buf.x, x_fp8), (buf.x_sf, x_sf), (buf.topk_idx, idx), (buf.topk_weights, w)):
-        t[:s_max].copy_(src)
+    _load_bucket(buf, x_fp8, x_sf, idx, w)
     y = torch.zeros((s_max, 4096), dtype=torch.bfloat16, device=cuda)
     log("full-shape graph: warm-up and capture at 2048 tokens")
-    mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
+    graph = _capture_bucket(mm, y, l1, l2, buf, "stages_fused_cuda_graph")
     ref_buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
-    for n, wide in ((s_max, True), (100, False), (1365, False), (1366, True), (100, False)):
-        log(f"  replay with runtime tokens={n}")
+    for n, wide in ((s_max, True), (100, False), (1365, False), (1366, True)):
+        tr = O.mega_moe_forward(x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1c, l2c, unpacked_weights=unpacked)
+        y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2)
+        for rep in range(2):
+            log(f"  replay {rep} with runtime tokens={n}")
+            y.fill_(7.0)
+            buf.cuda_graph_num_tokens.fill_(n)
+            graph.replay()
+            torch.cuda.synchronize()
+            meta = buf.scratch_view("meta").cpu()
+            assert int(meta[0]) == 6 * n and bool(meta[1] == 1) == wide, f"n={n}: kernel choice"
+            assert int(meta[3]) == 0, f"n={n}: status"
+            _oracle_prefix_check(buf, n, tr, y)
+            assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
+            assert torch.all(y[n:] == 7.0)
+
+
+def test_graph_decode_pipeline_bucket(mm, cuda, full_weights):
+    """The production decode bucket: the full shape (32 local of 256 global experts, H = 4096,
+    I = 2048, top-6) in a 1024-token bucket, so its 6144 tasks (<= 8192) put the one-launch
+    decode pipeline in the graph, which reads cuda_graph_num_tokens on the device. Replays at
+    n = 1024, 777, 128, 1, 0: the pipeline ran (it alone writes the per-block row maxima), no
+    bounded wait ran out (status 0) and its counters are back at zero; the routing of the prefix
+    is bit-exact and y[:n] within the bar of the oracle's, bitwise equal to an eager call on the
+    prefix; rows past n are untouched."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the decode pipeline runs on the whole 256-CU MI355X only")
+    l1, l2, l1c, l2c, unpacked = full_weights
+    s_max = 1024
+    x_fp8, x_sf, idx, w = make_tokens(s_max, 4096, 32, 6, seed=1234 + s_max, global_experts=256)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    assert buf.cuda_graph_max_tokens_per_rank == s_max and buf.num_max_tokens_per_rank == 1152
+    _load_bucket(buf, x_fp8, x_sf, idx, w)
+    y = torch.zeros((s_max, 4096), dtype=torch.bfloat16, device=cuda)
+    log("decode-bucket graph: warm-up and capture at 1024 tokens")
+    graph = _capture_bucket(mm, y, l1, l2, buf, "big_fused_cuda_graph")
+    ref_buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    for n in (1024, 777, 128, 1, 0):
+        tr = O.mega_moe_forward(x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1c, l2c,
+                                unpacked_weights=unpacked) if n > 0 else None
+        y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2) if n > 0 else None
+        for rep in range(2):
+            log(f"  replay {rep} with runtime tokens={n}")
+            y.fill_(7.0)
+            buf.scratch_view("pmax").fill_(-1.0)
+            buf.cuda_graph_num_tokens.fill_(n)
+            graph.replay()
+            torch.cuda.synchronize()
+            meta = buf.scratch_view("meta").cpu()
+            r = int(meta[0])
+            assert int(meta[3]) == 0, f"n={n}: a bounded wait ran out"
+            assert int(meta[1]) == 0, f"n={n}: GEMM1 of the pipeline leaves y, not h"
+            assert torch.all(buf.scratch_view("pipe").cpu() == 0), f"n={n}: pipeline counters"
+            if n > 0:
+                assert r == tr.routing.num_rows
+                assert bool((buf.scratch_view("pmax")[:r] >= 0).all()), f"n={n}: the pipeline ran"
+                _oracle_prefix_check(buf, n, tr, y)
+                assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
+            else:
+                assert r == 0
+            assert torch.all(y[n:] == 7.0), f"n={n}: rows past the prefix were written"
+
+
+def test_decode_pipeline_repeated_runs_bitwise(mm, cuda, full_weights):
+    """The c1 decode layer (one launch whose workgroups hand rows to each other through counters
+    and device-coherent loads) 50 times eagerly and 50 times as graph replays: every output is
+    bitwise the first one (a race in a hand-off would show as a differing bit). Stops at the
+    first mismatch."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the decode pipeline runs on the whole 256-CU MI355X only")
+    l1, l2 = full_weights[0], full_weights[1]
+    s = 1024
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, global_experts=256)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
+    _load_bucket(buf, x_fp8, x_sf, idx, w)
+    y = torch.empty((s, 4096), dtype=torch.bfloat16, device=cuda)
+    buf.scratch_view("pmax").fill_(-1.0)
+    mm.fp8_w8a8_mega_moe(y, l1, l2, buf)
+    torch.cuda.synchronize()
+    r = int(buf.scratch_view("meta")[0])
+    assert bool((buf.scratch_view("pmax")[:r] >= 0).all()), "the pipeline ran"
+    first = y.clone()
+    log("decode pipeline: 50 eager calls")
+    for i in range(50):
         y.fill_(7.0)
-        buf.cuda_graph_num_tokens.fill_(n)
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf)
+        torch.cuda.synchronize()
+        assert int(buf.scratch_view("meta")[3]) == 0, f"eager call {i}: status"
+        assert torch.equal(y.view(torch.int16), first.view(torch.int16)), f"eager call {i} differs"
+    graph = _capture_bucket(mm, y, l1, l2, buf, "big_fused_cuda_graph")
+    log("decode pipeline: 50 graph replays")
+    for i in range(50):
+        y.fill_(7.0)
         graph.replay()
         torch.cuda.synchronize()
-        meta = buf.scratch_view("meta").cpu()
-        assert int(meta[0]) == 6 * n and bool(meta[1] == 1) == wide, f"n={n}: kernel choice"
-        y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2)
-        torch.cuda.synchronize()
-        assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
-        assert torch.all(y[n:] == 7.0)
+        assert int(buf.scratch_view("meta")[3]) == 0, f"replay {i}: status"
+        assert torch.equal(y.view(torch.int16), first.view(torch.int16)), f"replay {i} differs"
+
+
+def test_decode_pipeline_failed_wait_is_reported(mm, cuda, full_weights, monkeypatch):
+    """MMOE_DEBUG_NO_WAIT, set from the host, makes every bounded wait of the decode pipeline give
+    up at its first poll (every kernel still runs to its end; the data it then reads are in
+    bounds, only possibly stale). The call's status counts those waits: mmoe_scratch_status
+    through the C ABI and last_call_status read it, and MEGAMOE_DEBUG_CHECK=1 makes the API raise.
+    The next ordinary call on the same scratch reports 0 again and is bitwise the first call."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the decode pipeline runs on the whole 256-CU MI355X only")
+    import ctypes
+
+    l1, l2 = full_weights[0], full_weights[1]
+    s = 1024
+    x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, global_experts=256)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048)
+    _load_bucket(buf, x_fp8, x_sf, idx, w)
+    y_ok = torch.empty((s, 4096), dtype=torch.bfloat16, device=cuda)
+    mm.fp8_w8a8_mega_moe(y_ok, l1, l2, buf)
+    assert mm.last_call_status(buf) == 0
+    lib = mm._capi.load()
+    log("decode pipeline with every bounded wait giving up at once (C ABI)")
+    y = torch.empty_like(y_ok)
+    args = mm._forward_args(y, l1, l2, None, buf, None, mm._capi.MMOE_SCHEDULE_AUTO)
+    args.debug_flags = mm._capi.MMOE_DEBUG_NO_WAIT
+    assert lib.mmoe_forward(ctypes.byref(args), mm._stream_handle()) == 0
+    out = torch.full((1,), -1, dtype=torch.int32, device=cuda)
+    assert lib.mmoe_scratch_status(buf.route_scratch.data_ptr(),
+                                   ctypes.cast(out.data_ptr(), ctypes.POINTER(ctypes.c_int32)),
+                                   mm._stream_handle()) == 0
+    torch.cuda.synchronize()
+    failed = int(out.item())
+    log(f"  status: {failed} waits ran out")
+    assert failed > 0
+    assert mm.last_call_status(buf) == failed
+    assert torch.all(buf.scratch_view("pipe").cpu() == 0), "counters back at zero all the same"
+    log("the same through the API with MEGAMOE_DEBUG_CHECK=1")
+    orig = mm._forward_args
+
+    def forced(*a, **k):
+        fa = orig(*a, **k)
+        fa.debug_flags = mm._capi.MMOE_DEBUG_NO_WAIT
+        return fa
+
+    monkeypatch.setenv("MEGAMOE_DEBUG_CHECK", "1")
+    monkeypatch.setattr(mm, "_forward_args", forced)
+    with pytest.raises(RuntimeError, match="bounded waits ran out"):
+        mm.fp8_w8a8_mega_moe(y, l1, l2, buf)
+    monkeypatch.setattr(mm, "_forward_args", orig)
+    y.fill_(7.0)
+    mm.fp8_w8a8_mega_moe(y, l1, l2, buf)  # checked: raises if the status is not 0
+    torch.cuda.synchronize()
+    assert mm.last_call_status(buf) == 0
+    assert torch.equal(y.view(torch.int16), y_ok.view(torch.int16))
+
+
+def _sampled_oracle_check(mm, buf, n, y, x_fp8, x_sf, idx, w, l1c, l2c, unpacked, seed):
+    """A token's output depends only on its own input and slots, so the oracle layer over a
+    sample of tokens is the oracle of those tokens in the whole layer: routing of the whole
+    prefix bit-exact (counts, output_index), and y of ~200 sampled tokens (with and without
+    local slots) within the bar."""
+    ref = O.route(idx[:n].cpu(), w[:n].cpu(), 32)
+    assert np.array_equal(buf.scratch_view("counts").cpu().numpy(), ref.counts), f"n={n}: counts"
+    assert np.array_equal(buf.scratch_view("output_index")[:n].cpu().numpy(),
+                          ref.output_index), f"n={n}: output_index"
+    gen = np.random.default_rng(seed)
+    sel = torch.from_numpy(np.sort(gen.choice(n, size=min(n, 200), replace=False))).long()
+    dsel = sel.to(x_fp8.device)
+    xs = x_fp8.view(torch.uint8)[dsel].cpu().view(torch.float8_e4m3fn)
+    tr = O.mega_moe_forward(xs, x_sf[dsel].cpu(), idx[dsel].cpu(), w[dsel].cpu(),
+                            l1c, l2c, unpacked_weights=unpacked)
+    d = O.calc_diff(y[sel.to(y.device)].cpu(), tr.y)
+    log(f"    n={n}: {sel.numel()} sampled tokens, calc_diff vs oracle {d:.3e}")
+    assert d <= CALC_DIFF_BAR
+    return ref
 
 
 def test_graph_ep_share_zero_rows(mm, cuda, full_weights):
     """An EP share (256 global experts, ~45% of the tokens without a local slot) in a
-    12288-token bucket: a full replay runs the WIDE kernels, whose idle workgroups write the
-    zero rows of the live tokens without a slot (the combine skips the chunks they claimed), a
-    short one the 8-wave kernels. Every replay is bitwise equal to an eager call on the same
-    prefix (zero rows included: y starts at 7.0), and rows past it are left alone."""
-    l1, l2 = full_weights[0], full_weights[1]
-    s_max = 12288
-    x_fp8, x_sf, idx, w = make_tokens(s_max, 4096, 32, 6, seed=444, global_experts=256)
+    65536-token bucket (~49K routed rows: 14 WIDE tiles a workgroup, the static deal): a full
+    replay runs the WIDE kernels, whose idle workgroups write the zero rows of live tokens without
+    a slot (the combine skips the chunks they claimed: the claim counter is past zero); a short
+    one the 8-wave kernels. Every replay: routing bit-exact and sampled tokens within the bar of
+    the oracle, bitwise equal to an eager call on the same prefix (zero rows included: y starts at
+    7.0), rows past the prefix left alone."""
+    l1, l2, l1c, l2c, unpacked = full_weights
+    s_max = 65536
+    x_fp8, x_sf, idx, w = _prefill_tokens_gpu(mm, s_max, 256, seed=444)
     buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
-    for t, src in ((buf.x, x_fp8), (buf.x_sf, x_sf), (buf.topk_idx, idx), (buf.topk_weights, w)):
-        t[:s_max].copy_(src)
+    _load_bucket(buf, x_fp8, x_sf, idx, w)
     y = torch.zeros((s_max, 4096), dtype=torch.bfloat16, device=cuda)
-    log("EP-share graph: warm-up and capture at 12288 tokens")
-    mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        mm.fp8_w8a8_mega_moe(y, l1, l2, buf, stages_fused_cuda_graph=True)
+    log("EP-share graph: warm-up and capture at 65536 tokens")
+    graph = _capture_bucket(mm, y, l1, l2, buf, "stages_fused_cuda_graph")
     ref_buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
     for n, wide in ((s_max, True), (1024, False), (s_max - 77, True)):
-        log(f"  replay with runtime tokens={n}")
-        y.fill_(7.0)
-        buf.cuda_graph_num_tokens.fill_(n)
-        graph.replay()
-        torch.cuda.synchronize()
-        assert bool(buf.scratch_view("meta")[1].item() == 1) == wide, f"n={n}: kernel choice"
         y_ref = torch.full((n, 4096), 7.0, dtype=torch.bfloat16, device=cuda)
         run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2, y=y_ref)
         torch.cuda.synchronize()
         unrouted = (idx[:n] < 0) | (idx[:n] >= 32)
-        zero_rows = unrouted.all(dim=1).to(cuda)
+        zero_rows = unrouted.all(dim=1)
         assert int(zero_rows.sum()) > n // 3, "many tokens without a local slot"
         assert torch.all(y_ref[zero_rows] == 0)
-        assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
-        assert torch.all(y[n:] == 7.0)
+        for rep in range(2):
+            log(f"  replay {rep} with runtime tokens={n}")
+            y.fill_(7.0)
+            buf.cuda_graph_num_tokens.fill_(n)
+            graph.replay()
+            torch.cuda.synchronize()
+            meta = buf.scratch_view("meta").cpu()
+            assert bool(meta[1].item() == 1) == wide, f"n={n}: kernel choice"
+            assert int(meta[3]) == 0, f"n={n}: status"
+            if wide:  # idle WIDE workgroups claimed zero-row chunks
+                assert int(buf.scratch_view("sched")[0, 9].item()) > 0, f"n={n}: zero rows claimed"
+            if rep == 0:
+                _sampled_oracle_check(mm, buf, n, y, x_fp8, x_sf, idx, w, l1c, l2c, unpacked, n)
+            assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
+            assert torch.all(y[n:] == 7.0)
+        del y_ref
 
 
 # ------------------------------------------------------------------ pre/post-process

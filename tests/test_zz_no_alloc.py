@@ -34,11 +34,24 @@ def _load(buf, x_fp8, x_sf, idx, w):
     buf.topk_weights[:s].copy_(w.to(buf.x.device))
 
 
+def _static_status(mm):
+    """mmoe_scratch_status of the static scratch (NULL route_scratch) on this device."""
+    out = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    st = mm._capi.load().mmoe_scratch_status(None, ctypes.cast(out.data_ptr(),
+                                                               ctypes.POINTER(ctypes.c_int32)),
+                                             mm._stream_handle())
+    assert st == 0, mm._capi.status_string(st)
+    return int(out.item())
+
+
 def test_static_scratch_matches_mmoe_forward(mm, cuda):
     e, hdim, inter, k = 32, 4096, 2048, 6
     l1, l2 = make_weights_gpu(e, hdim, inter, seed=4321, mm=mm)
-    # call 1: the decode config's size (1024 tokens, capacity 1152); call 2: a smaller input
-    for s, g, clamp in ((1024, 256, None), (200, 64, 1.0)):
+    # call 1: the decode config's size (1024 tokens, capacity 1152); call 2: the same capacity
+    # with every slot local (6144 rows: its fp32 y alone spans 50 MB of the static array); call 3:
+    # a smaller input, whose own layout would have put the pipeline counters inside call 2's y
+    # region had they not sat at offset 0 in every layout
+    for s, g, clamp in ((1024, 256, None), (1024, None, None), (200, 64, 1.0)):
         log(f"static scratch: S={s} clamp={clamp}")
         x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=77 + s, global_experts=g)
         buf = mm.get_symm_buffer_for_mega_moe(None, e, s, k, hdim, inter)
@@ -52,6 +65,7 @@ def test_static_scratch_matches_mmoe_forward(mm, cuda):
         st = _static_call(mm, y_got, l1, l2, buf, stats_got, clamp)
         assert st == 0, mm._capi.status_string(st)
         torch.cuda.synchronize()
+        assert _static_status(mm) == 0, f"S={s}: status of the static call"
         assert torch.equal(y_got.view(torch.int16), y_ref.view(torch.int16)), f"S={s}"
         assert torch.equal(stats_got, stats_ref)
         assert int(stats_ref.sum()) > 0
