@@ -11,14 +11,14 @@ random-init weights N(0, 1/sqrt(K)) quantised channelwise to e4m3.
 Timing: W warm-up layers, then K timed layers per config. Before every layer a 1 GiB buffer is
 read (a reduction) to flush the L2/MALL outside the timed events -- a read, so no dirty lines
 are left whose write-back would be charged to the layer; each layer is bracketed by HIP events
-on the stream it runs on. A second pass launches the stages separately with events between
-them to attribute time per kernel (roofline of the dominant kernel); when the whole layer is one
-launch (the decode pipeline), that launch's duration is taken from K (flush, layer) sequences
-minus K flushes, each between two events, since a kernel that follows a recorded event starts
-~5-6 us after the previous one ends (the per-call events of `value` include that gap). The CPU baseline is the
-repository's own oracle (a restatement of the reference's dequantise-and-matmul baseline) on
-all host cores: the whole c1 layer three times (median), and a bounded sample of each other
-config.
+on the stream it runs on (`value`: the median; it includes the ~5-6 us by which a kernel that
+follows a recorded event starts late). A second pass runs the same whole-layer calls through
+mmoe_forward_profile, which launches each of the layer's kernels with its own start and stop
+event (hipExtLaunchKernel: the dispatch's timestamps, as a kernel trace reads them): the
+per-kernel times (`stage_us`) and the dominant kernel's roofline come from there, so they are
+the kernels as they run inside the layer. The CPU baseline is the repository's own oracle (a
+restatement of the reference's dequantise-and-matmul baseline) on all host cores, over whole
+layers: c0 x10, c1 x3, c2/c3/c4 x1 (medians).
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -39,18 +39,17 @@ sys.path.insert(0, ROOT)
 E_LOCAL, HIDDEN, INTER, TOPK = 32, 4096, 2048, 6
 HBM_PEAK_BPS = 8.0e12       # MI355X HBM3E
 FP8_PEAK_FLOPS = 5.0e15     # MI355X dense FP8 MFMA
-ROUTE_IN_GEMM1_MAX_TASKS = 8192  # tasks (S*K) up to which GEMM1 routes in-kernel
 
 CONFIGS = {
-    "c0": dict(id=0, tokens=64, global_experts=None, routing="softmax",
+    "c0": dict(id=0, tokens=64, global_experts=None, routing="softmax", cpu_reps=10,
                workload="c0 T=64, 32 local experts (CPU-plumbing config)"),
-    "c1": dict(id=1, tokens=1024, global_experts=256, routing="softmax",
+    "c1": dict(id=1, tokens=1024, global_experts=256, routing="softmax", cpu_reps=3,
                workload="c1 decode T=128: 8x128 source tokens, top-6 of 256 experts, 0-31 kept"),
-    "c2": dict(id=2, tokens=32768, global_experts=256, routing="softmax",
+    "c2": dict(id=2, tokens=32768, global_experts=256, routing="softmax", cpu_reps=1,
                workload="c2 crossover T=4096: 8x4096 source tokens, top-6 of 256, 0-31 kept"),
-    "c3": dict(id=3, tokens=262144, global_experts=256, routing="softmax",
+    "c3": dict(id=3, tokens=262144, global_experts=256, routing="softmax", cpu_reps=1,
                workload="c3 prefill T=32768: 8x32768 source tokens, top-6 of 256, 0-31 kept"),
-    "c4": dict(id=4, tokens=8192, global_experts=None, routing="zipf",
+    "c4": dict(id=4, tokens=8192, global_experts=None, routing="zipf", cpu_reps=1,
                workload="c4 skew T=8192: top-6 i.i.d. Zipf(1.2) over 28 experts, 4 empty"),
 }
 HEADLINE = "c1"
@@ -158,24 +157,24 @@ class CpuOracle:
         self.unpacked = (O.marlin_unpack(self.l1[0], 2 * INTER, HIDDEN),
                          O.marlin_unpack(self.l2[0], HIDDEN, INTER))
 
-    def run(self, xc, sc, ic, wc, n_exp: int = E_LOCAL):
-        """One oracle layer over experts [0, n_exp) (the other slots masked to -1); returns
-        (seconds, routed rows, trace)."""
-        torch = self.torch
-        if n_exp < E_LOCAL:
-            # only the tokens with a slot in [0, n_exp): the others would add zero rows to the
-            # combine, whose cost grows with tokens rather than with routed rows
-            ic = torch.where(ic < n_exp, ic, torch.full_like(ic, -1))
-            keep = (ic >= 0).any(dim=1)
-            xc, sc, ic, wc = xc[keep], sc[keep], ic[keep], wc[keep]
-            l1 = (self.l1[0][:n_exp], self.l1[1][:n_exp])
-            l2 = (self.l2[0][:n_exp], self.l2[1][:n_exp])
-            unp = (self.unpacked[0][:n_exp], self.unpacked[1][:n_exp])
-        else:
-            l1, l2, unp = self.l1, self.l2, self.unpacked
+    def run(self, xc, sc, ic, wc):
+        """One whole oracle layer; returns (seconds, routed rows, trace). The trace keeps only
+        what the pipeline produces (no extra SwiGLU pass for the checks)."""
         t0 = time.perf_counter()
-        tr = self.O.mega_moe_forward(xc, sc, ic, wc, l1, l2, unpacked_weights=unp)
+        tr = self.O.mega_moe_forward(xc, sc, ic, wc, self.l1, self.l2, unpacked_weights=self.unpacked,
+                                     keep_y_act=False)
         return time.perf_counter() - t0, tr.routing.num_rows, tr
+
+
+def calc_diff_blocks(a, b, block: int = 16384) -> float:
+    """calc_diff = 1 - 2*sum(xy)/sum(x^2+y^2) in float64 (deep_gemm/testing/numeric.py:5-11),
+    summed over row blocks so that a 262,144-row output needs no whole float64 copies."""
+    num = den = 0.0
+    for i in range(0, a.shape[0], block):
+        x, y = a[i:i + block].double(), b[i:i + block].double()
+        num += float((x * y).sum())
+        den += float((x * x + y * y).sum())
+    return 0.0 if den == 0.0 else 1.0 - 2.0 * num / den
 
 
 def cpu_full_layer(oracle: CpuOracle, inputs, y_gpu, reps: int):
@@ -187,19 +186,68 @@ def cpu_full_layer(oracle: CpuOracle, inputs, y_gpu, reps: int):
         dt, rows, tr = oracle.run(xc, sc, ic, wc)
         times.append(dt)
     return dict(median_s=statistics.median(times), reps_s=[round(t, 3) for t in times],
-                rows=rows, parity_calc_diff=oracle.O.calc_diff(y_gpu.cpu(), tr.y))
+                rows=rows, parity_calc_diff=calc_diff_blocks(y_gpu.cpu(), tr.y))
 
 
-def cpu_sample(oracle: CpuOracle, inputs, total_rows: int, budget_s: float):
-    """A bounded sample of a larger config: the layer over experts [0, n), n chosen from one
-    timed expert to fit the budget, scaled to the whole layer by routed rows."""
-    xc, sc, ic, wc = (t.cpu() for t in inputs)
-    dt1, _, _ = oracle.run(xc, sc, ic, wc, 1)
-    n_exp = max(1, min(E_LOCAL, int(budget_s / max(dt1, 1e-3))))
-    dt, rows, _ = oracle.run(xc, sc, ic, wc, n_exp)
-    return dict(us_per_layer=round(dt * total_rows / max(rows, 1) * 1e6, 1),
-                sample=f"experts 0..{n_exp - 1}: {rows} of {total_rows} routed rows in "
-                       f"{dt:.2f} s, scaled by rows")
+class LayerProfiler:
+    """Whole-layer calls through mmoe_forward_profile: each kernel launch of the layer carries
+    its own start and stop event (hipExtLaunchKernel), so the events read the kernels' durations
+    inside the layer (the dispatch's timestamps). Events are made once through the HIP runtime
+    that the process already loaded."""
+
+    STAGES = {0: "route", 1: "gemm1", 2: "requant", 3: "gemm2", 4: "combine", 5: "pipeline"}
+    CAP = 16  # launches timed per call
+
+    def __init__(self, torch, mm, y, l1, l2, buf, steps: int):
+        import ctypes
+
+        self.ct = ctypes
+        self.torch, self.mm = torch, mm
+        path = next(line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line)
+        self.hip = ctypes.CDLL(path)
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        schedule = mm._eager_schedule(mm._large_opt_3stage_mode(), mm._large_opt_3stage_threshold(),
+                                      y.size(0))
+        self.args = mm._forward_args(y, l1, l2, None, buf, None, schedule)
+        self.keep = (y, l1, l2, buf)
+        self.events = []
+        for _ in range(steps):
+            arr = (ctypes.c_void_p * (2 * self.CAP))()
+            for j in range(2 * self.CAP):
+                ev = ctypes.c_void_p()
+                assert self.hip.hipEventCreate(ctypes.byref(ev)) == 0
+                arr[j] = ev.value
+            self.events.append(arr)
+        self.stages = [(ctypes.c_int32 * self.CAP)() for _ in range(steps)]
+        self.count = [ctypes.c_int32() for _ in range(steps)]
+
+    def launch(self, i: int) -> None:
+        ct = self.ct
+        st = self.mm._capi.load().mmoe_forward_profile(
+            ct.byref(self.args), self.mm._stream_handle(), ct.cast(self.events[i], ct.c_void_p),
+            self.CAP, self.stages[i], ct.byref(self.count[i]))
+        self.mm._capi.check(st, "mmoe_forward_profile")
+
+    def read(self):
+        """Per call: [(stage name, ms)] in launch order (after a synchronize)."""
+        out = []
+        for arr, stg, cnt in zip(self.events, self.stages, self.count):
+            step = []
+            for j in range(min(cnt.value, self.CAP)):
+                ms = self.ct.c_float()
+                assert self.hip.hipEventElapsedTime(self.ct.byref(ms), arr[2 * j], arr[2 * j + 1]) == 0
+                step.append((self.STAGES[stg[j]], ms.value))
+            out.append(step)
+        return out
+
+    def close(self) -> None:
+        for arr in self.events:
+            for ev in arr:
+                self.hip.hipEventDestroy(ev)
+        self.events = []
 
 
 def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
@@ -246,47 +294,23 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     log(f"  layer: median {med_ms * 1e3:.1f} us, min {min(ms) * 1e3:.1f} us")
 
     stage_ms = None
+    launches = None
     if not args.no_stage_timing:
-        # The stages as the layer runs them: when GEMM1 routes in-kernel (small task counts)
-        # routing and GEMM1 are one launch and are timed together.
-        # With the decode pipeline the whole layer is one launch.
-        call = mm.LayerCall(y, l1, l2, buf)
-        fused_route = s * TOPK <= ROUTE_IN_GEMM1_MAX_TASKS
-        if pipeline:
-            groups = [("pipeline", 0, 4)]
-        else:
-            groups = ([("gemm1", 0, 1)] if fused_route else [("route", 0, 0), ("gemm1", 1, 1)])
-            groups += [("requant", 2, 2), ("gemm2", 3, 3), ("combine", 4, 4)]
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(groups) + 1)]
-              for _ in range(args.steps)]
+        # The same whole-layer calls, each kernel launched with its own start and stop event:
+        # the kernels' durations inside the layer (a dual launch's kernel that returns at once
+        # counts in its stage; with the decode pipeline the layer is one launch).
+        prof = LayerProfiler(torch, mm, y, l1, l2, buf, args.steps)
         for i in range(args.steps):
             flush_cache()
-            ev[i][0].record()
-            for j, (_, first, last) in enumerate(groups):
-                call.run(first, last)
-                ev[i][j + 1].record()
+            prof.launch(i)
         torch.cuda.synchronize()
-        stage_ms = {gname: statistics.median(ev[i][j].elapsed_time(ev[i][j + 1])
-                                             for i in range(args.steps))
-                    for j, (gname, _, _) in enumerate(groups)}
-        log("  stages (median us): " + ", ".join(f"{k}={v * 1e3:.1f}" for k, v in stage_ms.items()))
-        if pipeline:
-            # One launch: its duration without the event marker in front of it (a kernel that
-            # follows a recorded event starts ~5-6 us after the previous one ends; back to back
-            # they start together): K x (flush, layer) minus K x flush, each sequence between
-            # two events, median of 3.
-            def seq_ms(with_layer: bool) -> float:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
-                for _ in range(args.steps):
-                    flush_cache()
-                    if with_layer:
-                        layer()
-                b.record()
-                torch.cuda.synchronize()
-                return a.elapsed_time(b) / args.steps
-            kernel_ms = statistics.median(seq_ms(True) - seq_ms(False) for _ in range(3))
-            log(f"  pipeline kernel without the event marker: {kernel_ms * 1e3:.1f} us")
+        per = prof.read()
+        prof.close()
+        names = [n for n in LayerProfiler.STAGES.values() if any(n == m for step in per for m, _ in step)]
+        stage_ms = {n: statistics.median(sum(ms for m, ms in step if m == n) for step in per) for n in names}
+        launches = [m for m, _ in per[0]]
+        log("  kernels in the layer (median us): " + ", ".join(f"{k}={v * 1e3:.1f}" for k, v in stage_ms.items())
+            + f"; launches {launches}")
 
     flops = 6.0 * rows * HIDDEN * INTER
     nbytes = algorithmic_bytes(rows, touched)
@@ -295,28 +319,32 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     roofline = None
     if stage_ms is not None:
         dom = "pipeline" if pipeline else max(("gemm1", "gemm2"), key=lambda k: stage_ms[k])
-        dom_ms = kernel_ms if pipeline else stage_ms[dom]
+        dom_ms = stage_ms[dom]
         dom_s = dom_ms * 1e-3
-        prof = profiled_traffic(name, dom)
-        timing = ("(flush + layer) - flush sequences: the one launch without the event marker"
-                  if pipeline else "events around the stage's launch")
+        prof_traffic = profiled_traffic(name, dom)
+        timing = ("the kernel's own start/stop events (hipExtLaunchKernel) in whole-layer calls, "
+                  "median over the steps")
         if bound == "hbm":
             achieved = nbytes[dom] / dom_s / 1e9
             roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1),
                             peak=HBM_PEAK_BPS / 1e9, unit="GB/s",
                             frac=round(achieved * 1e9 / HBM_PEAK_BPS, 4),
-                            traffic=prof[0] if prof else None,
+                            traffic=prof_traffic[0] if prof_traffic else None,
                             algorithmic_bytes=nbytes[dom], avg_us=round(dom_ms * 1e3, 2),
-                            timing=timing, traffic_source=prof[1] if prof else None)
+                            # the layer's bytes over the per-call event time (`value`, which also
+                            # holds the event marker's start delay)
+                            frac_of_layer_time=round(nbytes["layer"] / t_s / HBM_PEAK_BPS, 4),
+                            timing=timing, traffic_source=prof_traffic[1] if prof_traffic else None)
         else:
             kflops = 2.0 * rows * HIDDEN * {"gemm1": 2 * INTER, "gemm2": INTER, "pipeline": 3 * INTER}[dom]
             achieved = kflops / dom_s / 1e12
             roofline = dict(kernel=dom, bound="mfma", achieved=round(achieved, 1),
                             peak=FP8_PEAK_FLOPS / 1e12, unit="TFLOP/s",
                             frac=round(achieved * 1e12 / FP8_PEAK_FLOPS, 4),
-                            traffic=prof[0] if prof else None,
+                            traffic=prof_traffic[0] if prof_traffic else None,
                             algorithmic_flops=kflops, avg_us=round(dom_ms * 1e3, 2),
-                            timing=timing, traffic_source=prof[1] if prof else None)
+                            frac_of_layer_time=round(flops / t_s / FP8_PEAK_FLOPS, 4),
+                            timing=timing, traffic_source=prof_traffic[1] if prof_traffic else None)
     res = {
         "workload": cfg["workload"], "tokens": s, "routed_rows": rows, "touched_experts": touched,
         "largest_expert_rows": int(counts.max()),
@@ -326,6 +354,7 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
         "mfma_frac": round(flops / t_s / FP8_PEAK_FLOPS, 4),
         "layer_bound": bound, "algorithmic_bytes": nbytes["layer"], "flops": flops,
         "stage_us": None if stage_ms is None else {k: round(v * 1e3, 2) for k, v in stage_ms.items()},
+        "launches": launches,
         "roofline": roofline, "wall_s_timed_loop_incl_flush": round(wall, 4),
     }
     del buf
@@ -351,14 +380,14 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="c1,c2,c3,c4",
+    ap.add_argument("--configs", default="c0,c1,c2,c3,c4",
                     help="configs to time, comma-separated; the headline value is c1's (or the "
                          "first one's when c1 is not among them)")
     ap.add_argument("--config", default=None, choices=sorted(CONFIGS),
                     help="time this one config only (same as --configs NAME)")
-    ap.add_argument("--cpu-reps", type=int, default=3, help="CPU baseline reps of the c1 layer")
-    ap.add_argument("--cpu-sample-s", type=float, default=8.0,
-                    help="CPU seconds of the bounded oracle sample of each other config")
+    ap.add_argument("--cpu-reps", type=int, default=0,
+                    help="CPU baseline reps of every config's whole layer (0: c0 x10, c1 x3, "
+                         "c2-c4 x1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-timing", action="store_true")
     ap.add_argument("--calibrate-mib", type=int, default=0,
@@ -399,25 +428,23 @@ def main() -> int:
     for name in names:
         res, inputs, y = time_config(name, CONFIGS[name], l1, l2, args, torch, mm, flush_cache)
         if oracle is not None:
+            reps = args.cpu_reps or CONFIGS[name]["cpu_reps"]
+            log(f"  cpu baseline: the whole layer x{reps} on {torch.get_num_threads()} threads")
+            full = cpu_full_layer(oracle, inputs, y, reps)
+            base = dict(value=round(full["median_s"] * 1e6, 1), unit="us/layer",
+                        cores=torch.get_num_threads(), kind="port",
+                        sample=f"whole {name} layer ({full['rows']} routed rows), oracle "
+                               f"dequantise-and-matmul pipeline (K2 form) from FP8 inputs and "
+                               f"weights, median of {reps} reps {full['reps_s']} s",
+                        os_cpu_count=os.cpu_count(), torch_threads=torch.get_num_threads(),
+                        cpu_model=cpu_model(), parity_calc_diff=full["parity_calc_diff"])
+            res["cpu_us"] = base["value"]
+            res["cpu_sample"] = base["sample"]
+            res["cpu_parity_calc_diff"] = full["parity_calc_diff"]
             if name == headline:
-                log(f"  cpu baseline: the whole layer x{args.cpu_reps} on "
-                    f"{torch.get_num_threads()} threads")
-                full = cpu_full_layer(oracle, inputs, y, args.cpu_reps)
-                cpu = dict(value=round(full["median_s"] * 1e6, 1), unit="us/layer",
-                           cores=torch.get_num_threads(), kind="port",
-                           sample=f"whole {name} layer ({full['rows']} routed rows), oracle "
-                                  f"dequantise-and-matmul pipeline (K2 form) from FP8 inputs and "
-                                  f"weights, median of {args.cpu_reps} reps {full['reps_s']} s",
-                           os_cpu_count=os.cpu_count(), torch_threads=torch.get_num_threads(),
-                           cpu_model=cpu_model(), parity_calc_diff=full["parity_calc_diff"])
-                res["cpu_us"] = cpu["value"]
-                log(f"  cpu baseline: {cpu['value']} us/layer; parity calc_diff="
-                    f"{full['parity_calc_diff']:.2e}")
-            else:
-                smp = cpu_sample(oracle, inputs, res["routed_rows"], args.cpu_sample_s)
-                res["cpu_us"] = smp["us_per_layer"]
-                res["cpu_sample"] = smp["sample"]
-                log(f"  cpu sample: {smp['us_per_layer']} us/layer ({smp['sample']})")
+                cpu = base
+            log(f"  cpu baseline: {base['value']} us/layer; parity calc_diff="
+                f"{full['parity_calc_diff']:.2e}")
         per_config[name] = res
         del inputs, y
         torch.cuda.empty_cache()

@@ -10,6 +10,7 @@
 
 #include "../../include/megamoe_hip.h"
 #include "kernels.h"
+#include "launch.h"
 
 namespace {
 
@@ -203,6 +204,11 @@ int static_scratch_address(void** out) {
   return MMOE_OK;
 }
 
+// mmoe_forward_profile: the stage that the following launches of this host thread belong to.
+void mark_stage(int stage) {
+  if (mmoe::LaunchTimer* t = mmoe::launch_timer()) t->stage = stage;
+}
+
 int run_route(const mmoe_forward_args* a, const mmoe_scratch_layout& l, hipStream_t s) {
   const mmoe::RouteArgs r = forward_route_args(a, l);
   const int64_t tasks = static_cast<int64_t>(a->num_tokens) * a->num_topk;
@@ -210,6 +216,13 @@ int run_route(const mmoe_forward_args* a, const mmoe_scratch_layout& l, hipStrea
 }
 
 }  // namespace
+
+namespace mmoe {
+LaunchTimer*& launch_timer() {
+  static thread_local LaunchTimer* timer = nullptr;
+  return timer;
+}
+}  // namespace mmoe
 
 extern "C" {
 
@@ -336,6 +349,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
                                     runs(MMOE_STAGE_ROUTE) && runs(MMOE_STAGE_GEMM1) &&
                                     a->num_experts <= mmoe::gemm_route_max_experts();
   if (runs(MMOE_STAGE_ROUTE) && !route_in_gemm1) {
+    mark_stage(MMOE_STAGE_ROUTE);
     mmoe::RouteArgs r = forward_route_args(a, l);
     const int64_t tasks = static_cast<int64_t>(a->num_tokens) * a->num_topk;
     if (route_small_in_gemm1) r.fused_max_tasks = mmoe::gemm_route_max_tasks();
@@ -442,6 +456,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
       p.y = static_cast<uint16_t*>(a->y);
       combined = true;
     }
+    mark_stage(MMOE_STAGE_PIPELINE);
     if (mmoe::launch_decode_pipeline(p, cus, s) != hipSuccess) return MMOE_ERR_HIP;
   } else {
     // Eager calls whose bound selects WIDE by a small margin: the routing's largest expert row
@@ -451,6 +466,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     const int32_t* dual_rows = eager_dual ? at<int32_t>(ws, l.meta_offset) + 4 : rows_on_device;
     const int dual_min = eager_dual ? mmoe::gemm_eager_dual_min_largest()
                                     : mmoe::gemm_wide_min_rows(a->num_experts);
+    mark_stage(MMOE_STAGE_GEMM1);
     if (runs(MMOE_STAGE_GEMM1) &&
         mmoe::launch_grouped_gemm(g1, max_rows, cus, s, dual_rows, route_small_in_gemm1, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
@@ -458,18 +474,21 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     // a dual GEMM1 launch it finds out on the device which GEMM1 ran)
     const bool wide1 = mmoe::gemm_wide_selected(g1, max_rows);
     const bool dual1 = wide1 && dual_rows != nullptr;
+    mark_stage(MMOE_STAGE_REQUANT);
     if (runs(MMOE_STAGE_REQUANT) &&
         mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, g1.sw, at<float>(ws, l.amax_offset),
                              at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
                              at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, dest,
                              cus, s, dual1 ? dual_rows : nullptr, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
+    mark_stage(MMOE_STAGE_GEMM2);
     if (runs(MMOE_STAGE_GEMM2) &&
         mmoe::launch_grouped_gemm(g2, max_rows, cus, s, dual_rows, false, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
   }
 
   if (runs(MMOE_STAGE_COMBINE) && !combined) {
+    mark_stage(MMOE_STAGE_COMBINE);
     mmoe::CombineArgs c;
     memset(&c, 0, sizeof(c));
     c.y = static_cast<uint16_t*>(a->y);
@@ -508,6 +527,24 @@ int mmoe_scratch_status(const void* route_scratch, int32_t* out, void* stream) {
 
 int mmoe_forward(const mmoe_forward_args* a, void* stream) {
   return mmoe_forward_stages(a, MMOE_STAGE_ROUTE, MMOE_STAGE_COMBINE, stream);
+}
+
+int mmoe_forward_profile(const mmoe_forward_args* a, void* stream, void* const* events,
+                         int capacity, int32_t* stages, int32_t* num_launches) {
+  if (capacity < 0 || (capacity > 0 && events == nullptr)) return MMOE_ERR_ARGUMENT;
+  mmoe::LaunchTimer timer;
+  timer.events = reinterpret_cast<hipEvent_t const*>(events);
+  timer.stages = stages;
+  timer.capacity = capacity;
+  timer.count = 0;
+  timer.stage = MMOE_STAGE_ROUTE;
+  mmoe::LaunchTimer*& slot = mmoe::launch_timer();
+  mmoe::LaunchTimer* const outer = slot;
+  slot = &timer;
+  const int st = mmoe_forward_stages(a, MMOE_STAGE_ROUTE, MMOE_STAGE_COMBINE, stream);
+  slot = outer;
+  if (num_launches != nullptr) *num_launches = timer.count;
+  return st;
 }
 
 int mmoe_forward_static(const mmoe_forward_args* args, void* stream) {

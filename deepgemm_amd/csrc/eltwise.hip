@@ -6,6 +6,7 @@
 //   * row gather for the DeepEP-style preprocess, channelwise FP8 cast, Marlin pack.
 #include "common.cuh"
 #include "kernels.h"
+#include "launch.h"
 
 namespace mmoe {
 
@@ -363,12 +364,9 @@ hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw
   // resident): 397 us at 195,558 rows vs 470 us with 4 a CU
   const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 16);
   if (dual_rows != nullptr)
-    hipLaunchKernelGGL(requant_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, r);
-  else if (from_h)
-    hipLaunchKernelGGL(requant_kernel<1>, dim3(grid), dim3(kEltThreads), 0, stream, r);
-  else
-    hipLaunchKernelGGL(requant_kernel<0>, dim3(grid), dim3(kEltThreads), 0, stream, r);
-  return hipGetLastError();
+    return launch_kernel(requant_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+  if (from_h) return launch_kernel(requant_kernel<1>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+  return launch_kernel(requant_kernel<0>, dim3(grid), dim3(kEltThreads), 0, stream, r);
 }
 
 hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream) {
@@ -381,18 +379,17 @@ hipError_t launch_combine(const CombineArgs& c, int num_cus, hipStream_t stream)
     if (c.host_tokens >= static_cast<int64_t>(num_cus) * 16) {
       const int64_t items = c.host_tokens * ((nvec + kWave * 8 - 1) / (kWave * 8));
       const unsigned grid = grid_for(items, kEltWaves, static_cast<int64_t>(num_cus) * 8);
-      hipLaunchKernelGGL(combine_kernel<8>, dim3(grid), dim3(kEltThreads), 0, stream, c);
+      return launch_kernel(combine_kernel<8>, dim3(grid), dim3(kEltThreads), 0, stream, c);
     } else {
       const int64_t items = c.host_tokens * ((nvec + kWave * 2 - 1) / (kWave * 2));
       const unsigned grid = grid_for(items, kEltWaves, static_cast<int64_t>(num_cus) * 8);
-      hipLaunchKernelGGL(combine_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, c);
+      return launch_kernel(combine_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, c);
     }
   } else {
     if (c.skip_single != nullptr) return hipErrorInvalidValue;
     const unsigned grid = grid_for(c.host_tokens, 1, static_cast<int64_t>(num_cus) * 16);
-    hipLaunchKernelGGL(combine_scalar_kernel, dim3(grid), dim3(kEltThreads), 0, stream, c);
+    return launch_kernel(combine_scalar_kernel, dim3(grid), dim3(kEltThreads), 0, stream, c);
   }
-  return hipGetLastError();
 }
 
 hipError_t launch_gather_tasks(uint8_t* grouped_x, float* grouped_scale, const uint8_t* x,

@@ -46,6 +46,7 @@
 
 #include "common.cuh"
 #include "kernels.h"
+#include "launch.h"
 #include "route_wave.cuh"
 
 namespace mmoe {
@@ -1804,9 +1805,8 @@ hipError_t launch_wide(const GemmArgs& g, int max_rows, int num_cus, hipStream_t
       (static_cast<int64_t>(max_rows) / BM + g.num_experts) * ((g.n + kTileBN - 1) / kTileBN);
   int64_t grid = static_cast<int64_t>(num_cus) * W::kWavesPerSimd;  // workgroups a CU: 1 or 2
   if (grid > bound) grid = bound;
-  hipLaunchKernelGGL((wide_gemm_kernel<kGather, kSwiglu, BM>), dim3(static_cast<unsigned>(grid)),
-                     dim3(kWideThreads), W::kSmemBytes, stream, g);
-  return hipGetLastError();
+  return launch_kernel(wide_gemm_kernel<kGather, kSwiglu, BM>, dim3(static_cast<unsigned>(grid)),
+                       dim3(kWideThreads), W::kSmemBytes, stream, g);
 }
 
 template <bool kGather, bool kSwiglu, bool kAnyK>
@@ -1825,9 +1825,8 @@ hipError_t launch_engines_k(const GemmArgs& g, int max_rows, int num_cus, hipStr
                                                         : std::max(stream_items, tile_items);
   int64_t grid = num_cus;  // one 8-wave workgroup per CU
   if (grid > bound) grid = bound;
-  hipLaunchKernelGGL((grouped_gemm_kernel<kGather, kSwiglu, kAnyK>), dim3(static_cast<unsigned>(grid)),
-                     dim3(kGemmThreads), kSmemBytes, stream, g);
-  return hipGetLastError();
+  return launch_kernel(grouped_gemm_kernel<kGather, kSwiglu, kAnyK>, dim3(static_cast<unsigned>(grid)),
+                       dim3(kGemmThreads), kSmemBytes, stream, g);
 }
 
 template <bool kGather, bool kSwiglu>
@@ -1900,9 +1899,8 @@ hipError_t launch_decode_pipeline(const PipeArgs& p, int num_cus, hipStream_t st
     return hipErrorInvalidValue;
   const hipError_t err = ensure_dynamic_lds<&decode_pipeline_kernel>(kSmemBytes);
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(decode_pipeline_kernel, dim3(static_cast<unsigned>(num_cus)), dim3(kGemmThreads),
-                     kSmemBytes, stream, p);
-  return hipGetLastError();
+  return launch_kernel(decode_pipeline_kernel, dim3(static_cast<unsigned>(num_cus)), dim3(kGemmThreads),
+                       kSmemBytes, stream, p);
 }
 
 hipError_t launch_grouped_gemm(const GemmArgs& g, int max_rows, int num_cus, hipStream_t stream,

@@ -18,6 +18,7 @@
 //   * large: a count kernel (one workgroup per chunk, LDS histogram) and a scatter kernel
 //     (one workgroup per chunk) that rebuilds the expert offsets and its chunk base from the
 //     per-chunk counts itself, so no grid-wide barrier or separate scan launch is needed.
+#include "launch.h"
 #include "route_wave.cuh"
 
 namespace mmoe {
@@ -303,19 +304,16 @@ int64_t route_chunk_tasks(int64_t ntasks) {
 hipError_t launch_route(const RouteArgs& a, int64_t max_tasks, hipStream_t stream) {
   if (max_tasks <= 0) return hipSuccess;
   if (max_tasks <= kSmallWaves * kRouteChunk && a.num_experts <= kSmallMaxExperts) {
-    hipLaunchKernelGGL(route_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
-    return hipGetLastError();
+    return launch_kernel(route_small_kernel, dim3(1), dim3(kSmallThreads), 0, stream, a);
   }
   const int64_t chunk = route_chunk_tasks(max_tasks);
   const int64_t chunks = (max_tasks + chunk - 1) / chunk;
-  hipLaunchKernelGGL(route_count_kernel, dim3(static_cast<unsigned>(chunks)), dim3(kChunkThreads),
-                     0, stream, a, static_cast<int>(chunk));
-  hipError_t err = hipGetLastError();
+  const hipError_t err = launch_kernel(route_count_kernel, dim3(static_cast<unsigned>(chunks)),
+                                       dim3(kChunkThreads), 0, stream, a, static_cast<int>(chunk));
   if (err != hipSuccess) return err;
-  hipLaunchKernelGGL(route_chunk_scatter_kernel, dim3(static_cast<unsigned>(chunks)),
-                     dim3(kChunkThreads), 0, stream, a, static_cast<int>(chunk),
-                     static_cast<int>(chunks));
-  return hipGetLastError();
+  return launch_kernel(route_chunk_scatter_kernel, dim3(static_cast<unsigned>(chunks)),
+                       dim3(kChunkThreads), 0, stream, a, static_cast<int>(chunk),
+                       static_cast<int>(chunks));
 }
 
 }  // namespace mmoe

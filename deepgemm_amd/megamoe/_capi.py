@@ -18,6 +18,7 @@ MMOE_STATIC_SCRATCH_BYTES = 128 << 20
 MMOE_PIPE_INTS = 4928
 MMOE_SCRATCH_STATUS_OFFSET = MMOE_PIPE_INTS * 4 + 3 * 4
 MMOE_DEBUG_NO_WAIT = 1
+MMOE_STAGE_PIPELINE = 5
 MMOE_SCHEDULE_AUTO = 0
 MMOE_SCHEDULE_PERSISTENT = 1
 MMOE_SCHEDULE_STAGED = 2
@@ -103,6 +104,8 @@ SIGNATURES = {
     "mmoe_forward": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
     "mmoe_forward_static": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
     "mmoe_scratch_status": (ctypes.c_int, [c_p, ctypes.POINTER(c_i32), c_p]),
+    "mmoe_forward_profile": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p, c_p, ctypes.c_int,
+                                            ctypes.POINTER(c_i32), ctypes.POINTER(c_i32)]),
     "mmoe_route": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), c_p]),
     "mmoe_forward_stages": (ctypes.c_int, [ctypes.POINTER(ForwardArgs), ctypes.c_int,
                                            ctypes.c_int, c_p]),

@@ -231,6 +231,20 @@ int mmoe_forward_static(const mmoe_forward_args* args, void* stream);
 int mmoe_forward_stages(const mmoe_forward_args* args, int first_stage, int last_stage,
                         void* stream);
 
+#define MMOE_STAGE_PIPELINE 5 /* (mmoe_forward_profile) the one-launch decode pipeline: stages 0-4 */
+
+/* mmoe_forward with each kernel launch timed inside the whole layer call: launch i (launch
+ * order, i < capacity) goes out through hipExtLaunchKernel with events[2i] as its start and
+ * events[2i+1] as its stop event, which take the dispatch's own timestamps (the kernel's duration
+ * as a kernel trace reads it, and no event marker between the layer's kernels); stages[i] (may be
+ * NULL) = the MMOE_STAGE_* of launch i; *num_launches (may be NULL) = the call's launches (those
+ * past capacity run untimed). The events are hipEvent_t made by the caller; read them
+ * (hipEventElapsedTime) once the stream has passed them. Asynchronous like mmoe_forward, with the
+ * same results. For measurement only; it replaces the reference harness's timing of each call
+ * between two stream events (tests/test_mega_moe_dcu.py:326-341). */
+int mmoe_forward_profile(const mmoe_forward_args* args, void* stream, void* const* events,
+                         int capacity, int32_t* stages, int32_t* num_launches);
+
 /* Routing only (counts, offsets, output_index, row_token, row_weight, m_indices, stats) into
  * route_scratch: the route stage of mmoe_forward exposed for stage parity. The reference
  * computes the same in its route scan, deep_gemm/include/deep_gemm/impls/mega_moe_dcu.cuh:316-425,

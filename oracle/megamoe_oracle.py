@@ -301,13 +301,15 @@ def mega_moe_forward(x_fp8: torch.Tensor, x_sf: torch.Tensor, topk_idx, topk_wei
                      l1_weights, l2_weights, num_tokens: Optional[int] = None,
                      activation_clamp: Optional[float] = None,
                      stats: Optional[torch.Tensor] = None,
-                     unpacked_weights=None) -> ForwardTrace:
+                     unpacked_weights=None, keep_y_act: bool = True) -> ForwardTrace:
     """The whole layer on the CPU (fp32 dequant matmuls), K2-form numerics.
 
     ``l1_weights = (W1 Marlin [E,2I/16,H*16] e4m3, sw1 [E,2I] f32)``, ``l2_weights`` likewise
     with [E,H/16,I*16]; ``unpacked_weights`` may pass pre-unpacked row-major weights to skip
     the inverse permute. ``stats`` (int32 [E]) is accumulated in place like
-    cumulative_local_expert_recv_stats (mega_moe_dcu.cuh:418-425)."""
+    cumulative_local_expert_recv_stats (mega_moe_dcu.cuh:418-425). ``keep_y_act=False`` leaves
+    the trace's SwiGLU output (y before the requant) out: the pipeline itself does not need it
+    (the CPU baseline's timing)."""
     w1m, sw1 = l1_weights
     w2m, sw2 = l2_weights
     num_experts = w1m.shape[0]
@@ -333,7 +335,8 @@ def mega_moe_forward(x_fp8: torch.Tensor, x_sf: torch.Tensor, topk_idx, topk_wei
     act, act_s = swiglu_quant_k2(h, rw, activation_clamp)
     part = grouped_gemm_dequant(act, act_s, w2, sw2.cpu(), rt.m_indices, rt.offsets)
     y = combine(part, rt.output_index, s)
-    return ForwardTrace(rt, h, swiglu_k2(h, rw, activation_clamp), act, act_s, part, y)
+    y_act = swiglu_k2(h, rw, activation_clamp) if keep_y_act else None
+    return ForwardTrace(rt, h, y_act, act, act_s, part, y)
 
 
 # ----------------------------------------------------------------------------------------
