@@ -719,9 +719,9 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
 
 // TM row tiles of 32: BM/32 for a full tile; fewer (4, 2 or 1) for an expert's last tile of
 // at most 128, 64 or 32 rows (a fraction of the MFMAs and A traffic for the row remainder).
-template <bool kGather, bool kSwiglu, int BM, int TM>
+template <bool kGather, bool kSwiglu, int BM, int TM, typename Hook = NoHook>
 __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
-                          uint8_t* smem) {
+                          uint8_t* smem, const Hook& before_epilogue = Hook{}) {
   using W = WideShape<BM>;
   constexpr int kWideStage = W::kStage;
   constexpr int kWideTables = W::kTables;
@@ -741,13 +741,28 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   const int unit = active ? unit_raw : units - 1;  // a partial column block: any valid columns
   const int hk = lane >> 5;
 
-  // A: load i covers row i*32 + tid/8, piece tid % 8
+  // A: load i covers row i*32 + tid/8, piece tid % 8 (rows past mrows read row 0). GEMM1
+  // (gather): the row scales for the epilogue's table are loaded by the same threads, from the
+  // same tokens (the eight threads of a row read one word and write one LDS entry with the same
+  // value), all the tokens first and then all the scales, with no branch between them, ahead of
+  // the stages' loads, so that every wait the compiler places in the prologue is exact (a scale
+  // chain of its own, token -> scale, had been sunk behind all the stage loads and made the
+  // prologue wait for every one of them). GEMM2 loads one row scale a thread (no chain).
   const uint8_t* a_src[kALoads];
+  float a_rs[kALoads];
+  int64_t a_row[kALoads];
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) {
     const int r = i * kRowsPerLoad + (tid >> 3);
-    a_src[i] = a_row_ptr<kGather>(g, rs, row0 + (r < mrows ? r : 0)) + (tid & 7) * 16;
+    const int row = row0 + (r < mrows ? r : 0);
+    a_row[i] = kGather ? static_cast<int64_t>(rs.token(row)) : row;
   }
+#pragma unroll
+  for (int i = 0; i < kALoads; ++i) {
+    a_src[i] = g.a + a_row[i] * g.lda + (tid & 7) * 16;
+    a_rs[i] = kGather ? g.a_scale[a_row[i]] : 0.0f;
+  }
+  const float pre_xs = kGather ? 0.0f : g.a_scale[row0 + min(tid, mrows - 1)];
   const int a_dst0 = (tid >> 3) * kWideBK + (((tid & 7) ^ ((tid >> 4) & 7)) << 4);
   // two register sets: a stage's A is loaded one stage before it is written to LDS, which is
   // one stage before it is read
@@ -833,14 +848,14 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   };
   static_assert(kGroups == 2 * kALoads, "one A load and one A write per group");
 
-  // prologue: the epilogue's scales (thread t: row t's A scale, and the weight-row scale of
-  // its wave's column lane), A stages 0 and 1 into LDS, stage 2 into register set 0, B steps
-  // 0..3, the first operands; the loads of stages 0, 1 and 2 go out together (stage 0 through
-  // registers of the prologue's own), so that stage 2 is in before the first stage needs it.
-  // Rows past mrows take the last row's scale (never stored).
-  const float pre_xs = row_scale<kGather>(g, rs, row0 + min(tid, mrows - 1));
+  // prologue: the epilogue's scales (the row scales loaded with the row tokens above; thread
+  // t: the weight-row scale of its wave's column lane), A stages 0 and 1 into LDS, stage 2 into
+  // register set 0, B steps 0..3, the first operands; the loads of stages 0, 1 and 2 go out
+  // together (stage 0 through registers of the prologue's own), so that stage 2 is in before
+  // the first stage needs it.
   // GEMM2: row tid's output address (its part row, or its token's y row when the token has no
-  // other routed slot and direct rows are on); the switch and the row table load side by side
+  // other routed slot and direct rows are on); the switch and the row table load side by side.
+  // Rows past mrows take the last row's (never stored).
   int pre_dest = -1, pre_on = 0;
   if (!kSwiglu && g.y_direct != nullptr) {
     pre_on = *g.direct_flag;
@@ -861,9 +876,14 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     *reinterpret_cast<int4*>(smem + a_dst0 + i * kRowsPerLoad * kWideBK) = ra0[i];  // stage 0, buffer 0
 #pragma unroll
   for (int i = 0; i < kALoads; ++i) store_a(1, i, 1);
-  if (tid < BM) reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
+  if constexpr (kGather) {
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i) reinterpret_cast<float*>(smem + kWideTables)[i * kRowsPerLoad + (tid >> 3)] = a_rs[i];
+  } else if (tid < BM) {
+    reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
+  }
   reinterpret_cast<float*>(smem + kWideTables + W::kColScales)[tid] = pre_bs;
-  if (!kSwiglu && tid < BM) {
+  if (!kSwiglu && (BM == kWideThreads || tid < BM)) {
     const int prow = row0 + min(tid, mrows - 1);
     reinterpret_cast<uint64_t*>(smem + kWideTables + W::kAddrs)[tid] =
         pre_on != 0 && pre_dest >= 0 ? reinterpret_cast<uint64_t>(g.y_direct + static_cast<int64_t>(pre_dest) * g.n)
@@ -880,6 +900,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     stage(kt + 1, kWideRing == 4 ? 2 : 0, 1, 0);  // a ring of 2 refills the same two slots
   }
   // every wave has passed its last LDS read of A (the barrier that ended the last stage)
+  before_epilogue();
   if (!active) return;
   store_wide<kGather, kSwiglu, BM, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
 }
@@ -1677,7 +1698,7 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
   const int total = s_prefix[E];
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
   const RowSrc rs{g.row_token, g.sw.row_weight, 0};
-  auto run_item = [&](int t) {
+  auto run_item = [&](int t, const auto& before_epilogue) {
     const int e = expert_of_item(s_prefix, E, t);
     const int cnt = s_count[e];
     int mt, nb;
@@ -1685,13 +1706,13 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
     const int mrows = min(BM, cnt - mt * BM);
     const int row0 = s_off[e] + mt * BM;
     if (BM == 256 && mrows > 128)
-      wide_tile<kGather, kSwiglu, BM, (BM == 256 ? 8 : 4)>(g, rs, e, row0, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, BM, (BM == 256 ? 8 : 4)>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
     else if (mrows > 64)
-      wide_tile<kGather, kSwiglu, BM, 4>(g, rs, e, row0, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, BM, 4>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
     else if (mrows > 32)
-      wide_tile<kGather, kSwiglu, BM, 2>(g, rs, e, row0, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, BM, 2>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
     else
-      wide_tile<kGather, kSwiglu, BM, 1>(g, rs, e, row0, mrows, nb, smem);
+      wide_tile<kGather, kSwiglu, BM, 1>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
   };
   // One item at a time from the static deal or from the claims. Claiming only pays when a
   // workgroup has few items (the last round's granularity is then a large share of its work;
@@ -1723,9 +1744,13 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
       }
     }
     if (t < 0) break;
-    int pending = 0;  // thread 0: the claim for the item after this one, issued now
-    if (dynamic && threadIdx.x == 0 && ri < cl.nranges) pending = atomicAdd(&g.sched[cl.range(ri)], 1);
-    run_item(t);
+    // thread 0: the claim for the item after this one, issued when the tile's MFMAs are done
+    // (its latency hides behind the epilogue; issued at the tile's start, its result stayed live
+    // through the tile and was spilled, with a wait for every memory operation in flight)
+    int pending = 0;
+    run_item(t, [&]() {
+      if (dynamic && threadIdx.x == 0 && ri < cl.nranges) pending = atomicAdd(&g.sched[cl.range(ri)], 1);
+    });
     if (dynamic && threadIdx.x == 0) {
       int next = -1;
       if (ri < cl.nranges) {
