@@ -41,14 +41,21 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 // fast-math sigmoid of the reference's fused path (hardware exp2 and reciprocal:
 // deep_gemm/include/deep_gemm/common/mega_moe_dcu.cuh:89-98; the staged K2 uses __expf,
 // megamoe/dcu_megamoe_large_opt/K2_fused/k2_fused_ext.cu:328).
-__device__ __forceinline__ float swiglu_weighted(float g, float u, float w, bool has_clamp, float c) {
-  if (has_clamp) {
+// kClamp fixed at compile time: without a clamp the compiler emits none of its instructions
+// (chosen per element at run time, it had computed the clamp for every channel and selected).
+template <bool kClamp>
+__device__ __forceinline__ float swiglu_weighted_c(float g, float u, float w, float c) {
+  if constexpr (kClamp) {
     u = fminf(c, fmaxf(-c, u));
     g = fminf(c, g);
   }
   constexpr float kLog2E = 1.4426950408889634f;
   const float sig = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * kLog2E));
   return g * sig * u * w;
+}
+
+__device__ __forceinline__ float swiglu_weighted(float g, float u, float w, bool has_clamp, float c) {
+  return has_clamp ? swiglu_weighted_c<true>(g, u, w, c) : swiglu_weighted_c<false>(g, u, w, c);
 }
 
 __device__ __forceinline__ float clip_e4m3(float v) {

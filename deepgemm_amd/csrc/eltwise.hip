@@ -58,21 +58,21 @@ __device__ __forceinline__ uint4 ld_nt(const uint4* p) {
 }
 
 // channels 4q .. 4q+3 of row `row`
-template <bool kFromH>
+// (kClamp: the activation clamp, fixed per launch)
+template <bool kFromH, bool kClamp>
 __device__ __forceinline__ float4 requant_load(const RequantArgs& r, int64_t row, int q, float w) {
   if (!kFromH) return ld_nt(reinterpret_cast<const float4*>(static_cast<const float*>(r.src) + row * r.inter) + q);
   const uint16_t* h = static_cast<const uint16_t*>(r.src) + row * 2 * r.inter;
   const uint2 gb = ld_nt(reinterpret_cast<const uint2*>(h) + q);
   const uint2 ub = ld_nt(reinterpret_cast<const uint2*>(h + r.inter) + q);
-  const bool c = r.sw.has_clamp;
   const float cv = r.sw.clamp;
-  return make_float4(swiglu_weighted(bf16_to_f32(gb.x & 0xffff), bf16_to_f32(ub.x & 0xffff), w, c, cv),
-                     swiglu_weighted(bf16_to_f32(gb.x >> 16), bf16_to_f32(ub.x >> 16), w, c, cv),
-                     swiglu_weighted(bf16_to_f32(gb.y & 0xffff), bf16_to_f32(ub.y & 0xffff), w, c, cv),
-                     swiglu_weighted(bf16_to_f32(gb.y >> 16), bf16_to_f32(ub.y >> 16), w, c, cv));
+  return make_float4(swiglu_weighted_c<kClamp>(bf16_to_f32(gb.x & 0xffff), bf16_to_f32(ub.x & 0xffff), w, cv),
+                     swiglu_weighted_c<kClamp>(bf16_to_f32(gb.x >> 16), bf16_to_f32(ub.x >> 16), w, cv),
+                     swiglu_weighted_c<kClamp>(bf16_to_f32(gb.y & 0xffff), bf16_to_f32(ub.y & 0xffff), w, cv),
+                     swiglu_weighted_c<kClamp>(bf16_to_f32(gb.y >> 16), bf16_to_f32(ub.y >> 16), w, cv));
 }
 
-template <bool kFromH>
+template <bool kFromH, bool kClamp = false>
 __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
@@ -92,7 +92,7 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
 #pragma unroll
       for (int i = 0; i < kRequantGroups; ++i) {
         const int q = lane + i * kWave;
-        v[i] = q < groups ? requant_load<kFromH>(r, row, q, w) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[i] = q < groups ? requant_load<kFromH, kClamp>(r, row, q, w) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         m = abs_max4(m, v[i]);
       }
       m = wave_max(m);
@@ -103,11 +103,11 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
         if (q < groups) __builtin_nontemporal_store(pack_e4m3x4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), ar + q);
       }
     } else {
-      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, requant_load<kFromH>(r, row, q, w));
+      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, requant_load<kFromH, kClamp>(r, row, q, w));
       m = wave_max(m);
       const float inv = kE4m3Max / fmaxf(m, kAmaxFloor);
       for (int q = lane; q < groups; q += kWave) {
-        const float4 v = requant_load<kFromH>(r, row, q, w);
+        const float4 v = requant_load<kFromH, kClamp>(r, row, q, w);
         __builtin_nontemporal_store(pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv), ar + q);
       }
     }
@@ -128,13 +128,13 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
 // kMode 0: from y, 1: from h, 2: decided on the device (a dual GEMM1 launch; RequantArgs)
 template <int kMode>
 __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
-  if (kMode == 2 && *r.dual_rows >= r.dual_min_rows) {
-    requant_rows<true>(r, r.dest.row_dest != nullptr);
-  } else if (kMode == 2) {
-    requant_rows<false>(r, false);
-  } else {
-    requant_rows<kMode == 1>(r, r.dest.row_dest != nullptr);
-  }
+  // from h: the SwiGLU, with or without the clamp (a uniform branch on the launch's argument)
+  // (after a dual launch the direct rows go with the WIDE GEMMs only: from h)
+  const bool from_h = kMode == 1 || (kMode == 2 && *r.dual_rows >= r.dual_min_rows);
+  const bool direct = r.dest.row_dest != nullptr && (kMode != 2 || from_h);
+  if (from_h && r.sw.has_clamp) requant_rows<true, true>(r, direct);
+  else if (from_h) requant_rows<true, false>(r, direct);
+  else requant_rows<false>(r, direct);
 }
 
 // ---------------------------------------------------------------- combine
