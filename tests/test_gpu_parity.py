@@ -613,6 +613,43 @@ def test_decode_pipeline_many_experts(mm, cuda, e, s, g):
     del l1, l2
 
 
+def test_caller_scratch_reused_across_shapes(mm, cuda, full_weights):
+    """One caller-owned route_scratch, zero-filled once, serves mmoe_forward calls of different
+    shapes in turn through the C ABI: an all-local 1024-token call (6144 rows: its fp32 y spans
+    50 MB), a 200-token call, an all-local 4096-token prefill call (the WIDE kernels), and the
+    first call again. Each is bitwise equal to the same call on a fresh zero-filled scratch and
+    reports status 0, and the decode pipeline's counters read zero after each: they sit at
+    offset 0 in every layout, and every call leaves them zero."""
+    import ctypes
+
+    l1, l2 = full_weights[0], full_weights[1]
+    lib = mm._capi.load()
+    cases = ((1024, None), (200, 64), (4096, None), (1024, None))
+    bufs = [mm.get_symm_buffer_for_mega_moe(None, 32, s, 6, 4096, 2048) for s, _ in cases]
+    need = max(b.route_scratch.numel() for b in bufs)
+    shared = torch.zeros((need,), dtype=torch.int8, device=cuda)
+    status = torch.full((1,), -1, dtype=torch.int32, device=cuda)
+    for (s, g), buf in zip(cases, bufs):
+        log(f"shared scratch: S={s} global experts={g}")
+        x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=900 + s, global_experts=g)
+        _load_bucket(buf, x_fp8, x_sf, idx, w)
+        y_ref = torch.empty((s, 4096), dtype=torch.bfloat16, device=cuda)
+        mm.fp8_w8a8_mega_moe(y_ref, l1, l2, buf)
+        y = torch.full((s, 4096), 7.0, dtype=torch.bfloat16, device=cuda)
+        schedule = mm._eager_schedule(mm._large_opt_3stage_mode(), mm._large_opt_3stage_threshold(), s)
+        args = mm._forward_args(y, l1, l2, None, buf, None, schedule)
+        args.route_scratch = shared.data_ptr()
+        args.route_scratch_bytes = shared.numel()
+        assert lib.mmoe_forward(ctypes.byref(args), mm._stream_handle()) == 0
+        assert lib.mmoe_scratch_status(shared.data_ptr(), ctypes.cast(status.data_ptr(),
+                                       ctypes.POINTER(ctypes.c_int32)), mm._stream_handle()) == 0
+        torch.cuda.synchronize()
+        assert int(status.item()) == 0, f"S={s}: status"
+        pipe = shared[:mm._capi.MMOE_PIPE_INTS * 4].view(torch.int32)
+        assert torch.all(pipe.cpu() == 0), f"S={s}: pipeline counters left nonzero"
+        assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16)), f"S={s}: output"
+
+
 def test_layer_no_routed_rows(mm, cuda):
     """Every slot invalid -> y == 0 exactly (no partial contributes)."""
     s, e, hdim, inter = 10, 4, 256, 128
