@@ -361,6 +361,42 @@ def time_config(name: str, cfg: dict, l1, l2, args, torch, mm, flush_cache):
     return res, inputs, y
 
 
+def hipblaslt_gemm1(torch, rows: int, steps: int, flush_cache) -> dict:
+    """hipBLASLt's FP8 GEMM (torch._scaled_mm) at a config's GEMM1 shape, for comparison only:
+    [rows, H] x [H, 2I] e4m3 -> bf16, once with tensor-wise scales and once with per-row x
+    per-column scales (what the layer needs; its GEMM1 also gathers the rows, which this does
+    not). Median of `steps` calls, each after the cache flush, between two events."""
+    m = (rows + 255) // 256 * 256
+    g = torch.Generator(device="cuda").manual_seed(7)
+    a = (torch.randn((m, HIDDEN), generator=g, device="cuda") * 0.5).to(torch.float8_e4m3fn)
+    b = (torch.randn((2 * INTER, HIDDEN), generator=g, device="cuda") * 0.02).to(torch.float8_e4m3fn)
+    sa = torch.rand((m, 1), generator=g, device="cuda") + 0.5
+    sb = torch.rand((1, 2 * INTER), generator=g, device="cuda") + 0.5
+    one = torch.ones((), device="cuda")
+    out = {"rows": m, "n": 2 * INTER, "k": HIDDEN}
+    for mode, (x, y) in (("tensorwise", (one, one)), ("rowwise", (sa, sb))):
+        try:
+            torch._scaled_mm(a, b.t(), scale_a=x, scale_b=y, out_dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+        except Exception as exc:  # a scaling mode this torch/hipBLASLt does not offer
+            out[mode] = f"unsupported: {str(exc)[:100]}"
+            continue
+        ts = []
+        for _ in range(steps):
+            flush_cache()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            torch._scaled_mm(a, b.t(), scale_a=x, scale_b=y, out_dtype=torch.bfloat16)
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        med = statistics.median(ts)
+        out[mode] = {"us_median": round(med * 1e3, 1),
+                     "tflops": round(2.0 * m * 2 * INTER * HIDDEN / (med * 1e-3) / 1e12, 1)}
+        log(f"  hipBLASLt FP8 GEMM {m}x{2 * INTER}x{HIDDEN} {mode}: {out[mode]}")
+    return out
+
+
 def calibrate(torch, mib: int) -> dict:
     """Two known-size kernels for the rocprof byte counters of a profiling run: a read of
     `mib` MiB (a reduction: FETCH = mib MiB) and a device-to-device copy of `mib` MiB
@@ -390,6 +426,9 @@ def main() -> int:
                          "c2-c4 x1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-stage-timing", action="store_true")
+    ap.add_argument("--compare-hipblaslt", action="store_true",
+                    help="also time hipBLASLt's FP8 GEMM (torch._scaled_mm) at each config's GEMM1 "
+                         "shape (comparison only; reported under per_config.*.hipblaslt_gemm1)")
     ap.add_argument("--calibrate-mib", type=int, default=0,
                     help="after timing, read and copy a buffer of this many MiB once (known-size "
                          "kernels that calibrate rocprof byte counters)")
@@ -445,6 +484,8 @@ def main() -> int:
                 cpu = base
             log(f"  cpu baseline: {base['value']} us/layer; parity calc_diff="
                 f"{full['parity_calc_diff']:.2e}")
+        if args.compare_hipblaslt:
+            res["hipblaslt_gemm1"] = hipblaslt_gemm1(torch, res["routed_rows"], args.steps, flush_cache)
         per_config[name] = res
         del inputs, y
         torch.cuda.empty_cache()
