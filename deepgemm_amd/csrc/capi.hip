@@ -17,6 +17,8 @@ namespace {
 constexpr int kTokenAlignment = 384;  // deep_gemm/include/deep_gemm/layout/mega_moe_dcu.cuh:9
 constexpr int kMaxTopk = 16;
 constexpr int kMaxLayerExperts = 256;  // per-expert tile tables of the grouped GEMM
+// The kernels count routed rows (tokens x top-k) in 32-bit integers.
+constexpr int64_t kMaxRoutedRows = int64_t{1} << 30;
 
 int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
@@ -29,6 +31,7 @@ int check_common(int num_ranks, int num_experts, int num_max_tokens, int num_top
   if (num_topk <= 0 || num_topk > kMaxTopk) return MMOE_ERR_TOPK;
   if (num_experts / num_ranks <= 0 || num_experts / num_ranks > mmoe::kMaxExperts)
     return MMOE_ERR_UNSUPPORTED_SHAPE;
+  if (static_cast<int64_t>(num_max_tokens) * num_topk > kMaxRoutedRows) return MMOE_ERR_UNSUPPORTED_SHAPE;
   return MMOE_OK;
 }
 
@@ -285,7 +288,7 @@ const char* mmoe_status_string(int status) {
       return "route_scratch is too small for the requested DCU MegaMoE capacity";
     case MMOE_ERR_UNSUPPORTED_SHAPE:
       return "unsupported shape: hidden and intermediate must be multiples of 128, "
-             "1 <= experts <= 1024";
+             "1 <= local experts <= 1024 (256 for a forward call), num_max_tokens * num_topk <= 2^30";
     case MMOE_ERR_TOPK: return "num_topk must be in 1..16";
     case MMOE_ERR_SCHEDULE: return "unknown schedule override";
     case MMOE_ERR_HIP: return "HIP kernel launch failed";

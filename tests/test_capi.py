@@ -142,6 +142,8 @@ def test_debug_flags_are_validated():
     ((1, 32, 384, 6, 0, 2048), -4),
     ((1, 32, 384, 0, 4096, 2048), -10),
     ((1, 32, 384, 17, 4096, 2048), -10),
+    # routed rows are counted in 32-bit integers by the kernels: at most 2^30 of them
+    ((1, 32, (1 << 30) // 6 + 1, 6, 4096, 2048), -9),
 ])
 def test_layout_validation_codes(args, code):
     lib = _capi.load()
