@@ -473,13 +473,13 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     if (runs(MMOE_STAGE_GEMM1) &&
         mmoe::launch_grouped_gemm(g1, max_rows, cus, s, dual_rows, route_small_in_gemm1, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
-    // the WIDE GEMM1 leaves the bf16 pre-activation; the requant then applies the SwiGLU (after
-    // a dual GEMM1 launch it finds out on the device which GEMM1 ran)
+    // the WIDE GEMM1 leaves bf16 y, the 8-wave one f32 y (after a dual GEMM1 launch the requant
+    // finds out on the device which GEMM1 ran)
     const bool wide1 = mmoe::gemm_wide_selected(g1, max_rows);
     const bool dual1 = wide1 && dual_rows != nullptr;
     mark_stage(MMOE_STAGE_REQUANT);
     if (runs(MMOE_STAGE_REQUANT) &&
-        mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, g1.sw, at<float>(ws, l.amax_offset),
+        mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, at<float>(ws, l.amax_offset),
                              at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
                              at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, dest,
                              cus, s, dual1 ? dual_rows : nullptr, dual_min) != hipSuccess)

@@ -19,25 +19,24 @@ constexpr int kEltWaves = kEltThreads / kWave;
 // One wave per row: amax = max |y|; a = max(amax, 1e-4); act = e4m3(clip(y * (448/a)));
 // act_scale = a/448 (the K2 requant, megamoe/dcu_megamoe_large_opt/K2_fused/
 // k2_fused_ext.cu:341-364). A row of up to kRequantGroups*4*64 channels stays in registers
-// between the reduction and the quantization; a longer one is read twice. kFromH: y is made
-// here from GEMM1's bf16 pre-activation h (gate channels [0, I), up [I, 2I)) by the K2
-// SwiGLU x route weight (k2_fused_ext.cu:283-340) instead of being read as fp32.
+// between the reduction and the quantization; a longer one is read twice. y is GEMM1's SwiGLU
+// x route weight output (k2_fused_ext.cu:283-340, computed in GEMM1's epilogue): f32 from the
+// 8-wave kernels, bf16 from the WIDE kernel (kY16).
 constexpr int kRequantGroups = 8;  // float4 groups per lane held in registers
 
 struct RequantArgs {
-  const void* src;  // f32 y [rows, I], or bf16 h [rows, 2I] (kFromH)
-  SwigluEpilogue sw;
+  const void* src;  // f32 y [rows, I], or bf16 y [rows, I] (kY16)
   float* amax;
   int32_t* meta;
   uint8_t* act;
   float* act_scale;
   int inter;
   RowDest dest;
-  const int32_t* dual_rows;  // dual launches: from h iff *dual_rows >= dual_min_rows
+  const int32_t* dual_rows;  // dual launches: bf16 y iff *dual_rows >= dual_min_rows
   int dual_min_rows;
 };
 
-// Nontemporal accesses for the streams these kernels touch once: h / y and the partial rows are
+// Nontemporal accesses for the streams these kernels touch once: y and the partial rows are
 // read once, act is written once and read by GEMM2 from HBM anyway at prefill sizes. At c3 the
 // requant went from 405 to 379 us and the combine from 427 to 410 us (same box, alternating
 // builds); nontemporal stores of the combine's y rows were slower (436 us), so those stay plain.
@@ -58,32 +57,25 @@ __device__ __forceinline__ uint4 ld_nt(const uint4* p) {
 }
 
 // channels 4q .. 4q+3 of row `row`
-// (kClamp: the activation clamp, fixed per launch)
-template <bool kFromH, bool kClamp>
-__device__ __forceinline__ float4 requant_load(const RequantArgs& r, int64_t row, int q, float w) {
-  if (!kFromH) return ld_nt(reinterpret_cast<const float4*>(static_cast<const float*>(r.src) + row * r.inter) + q);
-  const uint16_t* h = static_cast<const uint16_t*>(r.src) + row * 2 * r.inter;
-  const uint2 gb = ld_nt(reinterpret_cast<const uint2*>(h) + q);
-  const uint2 ub = ld_nt(reinterpret_cast<const uint2*>(h + r.inter) + q);
-  const float cv = r.sw.clamp;
-  return make_float4(swiglu_weighted_c<kClamp>(bf16_to_f32(gb.x & 0xffff), bf16_to_f32(ub.x & 0xffff), w, cv),
-                     swiglu_weighted_c<kClamp>(bf16_to_f32(gb.x >> 16), bf16_to_f32(ub.x >> 16), w, cv),
-                     swiglu_weighted_c<kClamp>(bf16_to_f32(gb.y & 0xffff), bf16_to_f32(ub.y & 0xffff), w, cv),
-                     swiglu_weighted_c<kClamp>(bf16_to_f32(gb.y >> 16), bf16_to_f32(ub.y >> 16), w, cv));
+template <bool kY16>
+__device__ __forceinline__ float4 requant_load(const RequantArgs& r, int64_t row, int q) {
+  if (!kY16) return ld_nt(reinterpret_cast<const float4*>(static_cast<const float*>(r.src) + row * r.inter) + q);
+  const uint2 b = ld_nt(reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(r.src) + row * r.inter) + q);
+  return make_float4(bf16_to_f32(b.x & 0xffff), bf16_to_f32(b.x >> 16), bf16_to_f32(b.y & 0xffff),
+                     bf16_to_f32(b.y >> 16));
 }
 
-template <bool kFromH, bool kClamp = false>
+template <bool kY16>
 __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int rows = r.meta[0];
   const int groups = r.inter >> 2;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
-    r.meta[1] = kFromH ? 1 : 0;
+    r.meta[1] = kY16 ? 1 : 0;
     if (r.dest.meta_flag != nullptr) *r.dest.meta_flag = direct ? 1 : 0;
   }
   for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
-    const float w = kFromH ? r.sw.row_weight[row] : 0.0f;
     const int tok = direct ? r.dest.row_token[row] : 0;
     uint32_t* ar = reinterpret_cast<uint32_t*>(r.act + static_cast<int64_t>(row) * r.inter);
     float m = 0.0f;
@@ -92,7 +84,7 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
 #pragma unroll
       for (int i = 0; i < kRequantGroups; ++i) {
         const int q = lane + i * kWave;
-        v[i] = q < groups ? requant_load<kFromH, kClamp>(r, row, q, w) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[i] = q < groups ? requant_load<kY16>(r, row, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         m = abs_max4(m, v[i]);
       }
       m = wave_max(m);
@@ -103,11 +95,11 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
         if (q < groups) __builtin_nontemporal_store(pack_e4m3x4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), ar + q);
       }
     } else {
-      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, requant_load<kFromH, kClamp>(r, row, q, w));
+      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, requant_load<kY16>(r, row, q));
       m = wave_max(m);
       const float inv = kE4m3Max / fmaxf(m, kAmaxFloor);
       for (int q = lane; q < groups; q += kWave) {
-        const float4 v = requant_load<kFromH, kClamp>(r, row, q, w);
+        const float4 v = requant_load<kY16>(r, row, q);
         __builtin_nontemporal_store(pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv), ar + q);
       }
     }
@@ -125,15 +117,14 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
   }
 }
 
-// kMode 0: from y, 1: from h, 2: decided on the device (a dual GEMM1 launch; RequantArgs)
+// kMode 0: from f32 y, 1: from bf16 y, 2: decided on the device (a dual GEMM1 launch;
+// RequantArgs)
 template <int kMode>
 __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
-  // from h: the SwiGLU, with or without the clamp (a uniform branch on the launch's argument)
-  // (after a dual launch the direct rows go with the WIDE GEMMs only: from h)
-  const bool from_h = kMode == 1 || (kMode == 2 && *r.dual_rows >= r.dual_min_rows);
-  const bool direct = r.dest.row_dest != nullptr && (kMode != 2 || from_h);
-  if (from_h && r.sw.has_clamp) requant_rows<true, true>(r, direct);
-  else if (from_h) requant_rows<true, false>(r, direct);
+  // (after a dual launch the direct rows go with the WIDE GEMMs only: bf16 y)
+  const bool y16 = kMode == 1 || (kMode == 2 && *r.dual_rows >= r.dual_min_rows);
+  const bool direct = r.dest.row_dest != nullptr && (kMode != 2 || y16);
+  if (y16) requant_rows<true>(r, direct);
   else requant_rows<false>(r, direct);
 }
 
@@ -349,23 +340,22 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 
 }  // namespace
 
-hipError_t launch_requant(const void* src, bool from_h, const SwigluEpilogue& sw, float* amax,
-                          int32_t* meta, uint8_t* act, float* act_scale, int64_t max_rows,
-                          int inter, const RowDest& dest, int num_cus, hipStream_t stream,
-                          const int32_t* dual_rows, int dual_min_rows) {
+hipError_t launch_requant(const void* src, bool y16, float* amax, int32_t* meta, uint8_t* act,
+                          float* act_scale, int64_t max_rows, int inter, const RowDest& dest,
+                          int num_cus, hipStream_t stream, const int32_t* dual_rows,
+                          int dual_min_rows) {
   if (max_rows <= 0) return hipSuccess;
   if (inter % 4) return hipErrorInvalidValue;
-  if ((from_h || dual_rows != nullptr) && sw.row_weight == nullptr) return hipErrorInvalidValue;
   if (dest.row_dest != nullptr && (dest.row_token == nullptr || dest.output_index == nullptr ||
                                    dest.topk < 1 || dest.topk > kWave))
     return hipErrorInvalidValue;
-  const RequantArgs r{src, sw, amax, meta, act, act_scale, inter, dest, dual_rows, dual_min_rows};
+  const RequantArgs r{src, amax, meta, act, act_scale, inter, dest, dual_rows, dual_min_rows};
   // grid of up to 16 workgroups a CU (one row per wave in flight; the hardware keeps what fits
   // resident): 397 us at 195,558 rows vs 470 us with 4 a CU
   const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 16);
   if (dual_rows != nullptr)
     return launch_kernel(requant_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, r);
-  if (from_h) return launch_kernel(requant_kernel<1>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+  if (y16) return launch_kernel(requant_kernel<1>, dim3(grid), dim3(kEltThreads), 0, stream, r);
   return launch_kernel(requant_kernel<0>, dim3(grid), dim3(kEltThreads), 0, stream, r);
 }
 

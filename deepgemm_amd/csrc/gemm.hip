@@ -640,11 +640,9 @@ struct WideShape {
 // free 32 KB A buffer (64 rows x 128 bytes, 16-byte piece p of row r at p ^ ((r / 2) % 8):
 // conflict-free both ways); each pass of 64 rows then leaves as whole 16-byte pieces, 8 rows
 // per store instruction.
-// GEMM1 (kGemm1) writes the pre-activation h = bf16(acc * x_scale * w_scale) [rows, 2I] with
-// gate channels in [0, I) and up channels in [I, 2I) (the staged K1 output); GEMM2 writes the
-// bf16 partials (-0 as +0) to the row addresses of the tile's table: its part row, or for a
-// row whose token has no other routed slot its y row (row_dest).
-template <bool kGather, bool kGemm1, int BM, int TM>
+// GEMM2 writes the bf16 partials (-0 as +0) to the row addresses of the tile's table: its part
+// row, or for a row whose token has no other routed slot its y row (row_dest).
+template <int BM, int TM>
 __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[TM][2], int row0,
                                            int mrows, int unit, uint8_t* stage,
                                            const uint8_t* table) {
@@ -654,7 +652,7 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
   const int rl = lane & 31, hk = lane >> 5;
   const float* s_xs = reinterpret_cast<const float*>(table);
   const float* s_bs = reinterpret_cast<const float*>(table + W::kColScales) + (tid / kWave) * kStreamUnit;
-  const uint64_t* s_addr = reinterpret_cast<const uint64_t*>(table + W::kAddrs);  // GEMM2
+  const uint64_t* s_addr = reinterpret_cast<const uint64_t*>(table + W::kAddrs);
   float4 bs[2][4];
 #pragma unroll
   for (int tn = 0; tn < 2; ++tn)
@@ -662,11 +660,7 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
     for (int q = 0; q < 4; ++q) bs[tn][q] = *reinterpret_cast<const float4*>(s_bs + tn * 32 + q * 8 + hk * 4);
   uint8_t* wlds = stage + (tid / kWave) * 8192;
   const int piece = lane & 7;
-  // GEMM1: pieces 0-3 are gate channels unit*32 + 8p, pieces 4-7 the up channels
-  const int64_t ld = kGemm1 ? 2 * static_cast<int64_t>(g.sw.inter) : g.n;
-  const int col = kGemm1 ? (piece < 4 ? unit * 32 + piece * 8 : g.sw.inter + unit * 32 + (piece - 4) * 8)
-                         : unit * 64 + piece * 8;
-  uint16_t* out = (kGemm1 ? reinterpret_cast<uint16_t*>(g.sw.y) : g.c) + static_cast<int64_t>(row0) * ld + col;
+  const int col = unit * 64 + piece * 8;
 #pragma unroll
   for (int pass = 0; pass < (TM + 1) / 2; ++pass) {
 #pragma unroll
@@ -680,9 +674,9 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float4 ws = bs[tn][q];
-          // GEMM2: the scale product as fma(., ., +0), the same rounding, but a zero is +0 (the
+          // the scale product as fma(., ., +0), the same rounding, but a zero is +0 (the
           // combine's sum from +0 writes +0 too, so a y row written here matches it bitwise)
-          auto scaled = [&](float a, float w) { return kGemm1 ? a * xs * w : __builtin_fmaf(a * xs, w, 0.0f); };
+          auto scaled = [&](float a, float w) { return __builtin_fmaf(a * xs, w, 0.0f); };
           const uint32_t lo = pack_bf16x2(scaled(acc[tm][tn][4 * q], ws.x), scaled(acc[tm][tn][4 * q + 1], ws.y));
           const uint32_t hi = pack_bf16x2(scaled(acc[tm][tn][4 * q + 2], ws.z), scaled(acc[tm][tn][4 * q + 3], ws.w));
           // columns tn*32 + 8q + 4hk .. +4 -> bytes 64tn + 16q + 8hk: piece 4tn + q, half hk
@@ -697,21 +691,85 @@ __device__ __forceinline__ void store_wide(const GemmArgs& g, const v16f (&acc)[
     for (int i = 0; i < 8; ++i) {
       const int rr = i * 8 + (lane >> 3);
       val[i] = *reinterpret_cast<const int4*>(wlds + rr * 128 + ((piece ^ ((rr >> 1) & 7)) << 4));
-      if (!kGemm1) base[i] = s_addr[pass * 64 + rr];
+      base[i] = s_addr[pass * 64 + rr];
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int grow = pass * 64 + i * 8 + (lane >> 3);
-      if (kGemm1) {
-        if (grow < mrows) *reinterpret_cast<int4*>(out + grow * ld) = val[i];
-      } else {
-        // the row's address from the table (its part row or its token's y row); a global (not
-        // flat) store: a flat one would also hold up the LDS counter. Nontemporal: the rows are
-        // read once, by the combine (c3 -25 us; the same hint on GEMM1's h stores was slower)
-        const i32x4 v = {val[i].x, val[i].y, val[i].z, val[i].w};
-        if (grow < mrows)
-          __builtin_nontemporal_store(v, (__attribute__((address_space(1))) i32x4*)(base[i] + col * 2));
+      // the row's address from the table (its part row or its token's y row); a global (not
+      // flat) store: a flat one would also hold up the LDS counter. Nontemporal: the rows are
+      // read once, by the combine (c3 -25 us)
+      const i32x4 v = {val[i].x, val[i].y, val[i].z, val[i].w};
+      if (grow < mrows)
+        __builtin_nontemporal_store(v, (__attribute__((address_space(1))) i32x4*)(base[i] + col * 2));
+    }
+    // the next pass's LDS writes follow these reads in the wave's own (in-order) LDS queue
+  }
+}
+
+// Epilogue of a WIDE GEMM1 tile with the SwiGLU: the wave's unit holds the gate channels
+// unit*32 + c (column tile 0) and the up channels of the same c (column tile 1), so lane l has,
+// for token row tm*32 + l%32, four runs of 4 channels 8q + 4*(l/32) .. + 4 of both. Per channel:
+// g = bf16(acc_g * x_scale * w_scale_g) and u = bf16(acc_u * x_scale * w_scale_u) (the staged
+// K1 output h, rounded like its stores), then y = SwiGLU(g, u) x route weight (the K2 formula,
+// with the activation clamp when kClamp) and y rounded to bf16: bf16 y [rows, I] for the
+// requant, half of h's bytes. Each 4-channel run is one 8-byte write into the wave's 4 KB LDS
+// slice (64 rows x 64 bytes, 16-byte piece p of row r at p ^ ((r / 4) % 4)); a pass of 64 rows
+// leaves as 16-byte pieces, 16 rows per store instruction.
+template <bool kClamp, int BM, int TM>
+__device__ __forceinline__ void store_wide_swiglu(const GemmArgs& g, const v16f (&acc)[TM][2], int row0,
+                                                  int mrows, int unit, uint8_t* stage,
+                                                  const uint8_t* table) {
+  using W = WideShape<BM>;
+  const int tid = opaque_tid();
+  const int lane = tid & (kWave - 1);
+  const int rl = lane & 31, hk = lane >> 5;
+  const float* s_xs = reinterpret_cast<const float*>(table);
+  const float* s_rw = reinterpret_cast<const float*>(table + W::kAddrs);  // route weights
+  const float* s_bs = reinterpret_cast<const float*>(table + W::kColScales) + (tid / kWave) * kStreamUnit;
+  float4 bs[2][4];
+#pragma unroll
+  for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bs[tn][q] = *reinterpret_cast<const float4*>(s_bs + tn * 32 + q * 8 + hk * 4);
+  uint8_t* wlds = stage + (tid / kWave) * 4096;
+  const int64_t ld = g.sw.inter;
+  uint16_t* out = reinterpret_cast<uint16_t*>(g.sw.y) + static_cast<int64_t>(row0) * ld + unit * 32 + (lane & 3) * 8;
+  const float cv = g.sw.clamp;
+#pragma unroll
+  for (int pass = 0; pass < (TM + 1) / 2; ++pass) {
+#pragma unroll
+    for (int t2 = 0; t2 < (TM > 1 ? 2 : 1); ++t2) {  // TM = 1: one row tile, rows 32-63 unused
+      const int tm = pass * 2 + t2;
+      const float xs = s_xs[tm * 32 + rl];
+      const float rw = s_rw[tm * 32 + rl];
+      const int r = t2 * 32 + rl;  // row within the pass
+      const int rkey = (r >> 2) & 3;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 wg = bs[0][q], wu = bs[1][q];
+        const v16f& ag = acc[tm][0];
+        const v16f& au = acc[tm][1];
+        const float y0 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q] * xs * wg.x), bf16_round(au[4 * q] * xs * wu.x), rw, cv);
+        const float y1 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q + 1] * xs * wg.y), bf16_round(au[4 * q + 1] * xs * wu.y), rw, cv);
+        const float y2 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q + 2] * xs * wg.z), bf16_round(au[4 * q + 2] * xs * wu.z), rw, cv);
+        const float y3 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q + 3] * xs * wg.w), bf16_round(au[4 * q + 3] * xs * wu.w), rw, cv);
+        // channels 8q + 4hk .. +4 -> bytes 16q + 8hk of the row: piece q, half hk
+        *reinterpret_cast<uint2*>(wlds + r * 64 + ((q ^ rkey) << 4) + hk * 8) =
+            make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
       }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's LDS writes before its reads
+    int4 val[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = i * 16 + (lane >> 2);
+      val[i] = *reinterpret_cast<const int4*>(wlds + rr * 64 + (((lane & 3) ^ ((rr >> 2) & 3)) << 4));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int grow = pass * 64 + i * 16 + (lane >> 2);
+      if (grow < mrows) *reinterpret_cast<int4*>(out + grow * ld) = val[i];
     }
     // the next pass's LDS writes follow these reads in the wave's own (in-order) LDS queue
   }
@@ -861,6 +919,8 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     pre_on = *g.direct_flag;
     pre_dest = g.row_dest[row0 + min(tid, mrows - 1)];
   }
+  // GEMM1: row tid's route weight (the SwiGLU epilogue's)
+  const float pre_rw = kSwiglu ? g.sw.row_weight[row0 + min(tid, mrows - 1)] : 0.0f;
   const float pre_bs = g.b_scale[static_cast<int64_t>(e) * g.n + weight_row<kSwiglu>(g, unit, kStreamUnit, lane)];
   int4 ra0[kALoads];
 #pragma unroll
@@ -883,6 +943,7 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
     reinterpret_cast<float*>(smem + kWideTables)[tid] = pre_xs;
   }
   reinterpret_cast<float*>(smem + kWideTables + W::kColScales)[tid] = pre_bs;
+  if (kSwiglu && (BM == kWideThreads || tid < BM)) reinterpret_cast<float*>(smem + kWideTables + W::kAddrs)[tid] = pre_rw;
   if (!kSwiglu && (BM == kWideThreads || tid < BM)) {
     const int prow = row0 + min(tid, mrows - 1);
     reinterpret_cast<uint64_t*>(smem + kWideTables + W::kAddrs)[tid] =
@@ -902,7 +963,12 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
   // every wave has passed its last LDS read of A (the barrier that ended the last stage)
   before_epilogue();
   if (!active) return;
-  store_wide<kGather, kSwiglu, BM, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
+  if constexpr (kSwiglu) {
+    if (g.sw.has_clamp) store_wide_swiglu<true, BM, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
+    else store_wide_swiglu<false, BM, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
+  } else {
+    store_wide<BM, TM>(g, acc, row0, mrows, unit, smem, smem + kWideTables);
+  }
 }
 
 // ------------------------------------------------------------------ in-kernel routing

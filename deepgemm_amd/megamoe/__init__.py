@@ -283,8 +283,7 @@ class SymmBuffer:
         those rows' part is not written; meta[2] == 1 then), sched and pipe (the GEMMs' work
         counters, zero between calls), pmax (per row, max |y| of each 64-column block of GEMM1's
         output; written by the one-launch decode pipeline only). When meta[1] == 1 the GEMM1 of
-        the call left the bf16 pre-activation instead of y, in the same bytes: view it as h
-        ([rows, 2I], gate channels then up channels)."""
+        the call (the WIDE kernel) left y in bf16, in the same bytes: view it as y16."""
         l = self.scratch_layout
         e, t, k = self.num_experts, self.num_max_tokens_per_rank, self.num_topk
         rows = int(l.row_capacity if num_rows is None else num_rows)
@@ -299,7 +298,7 @@ class SymmBuffer:
             "act_scale": (l.act_scale_offset, torch.float32, (rows,)),
             "amax": (l.amax_offset, torch.float32, (rows,)),
             "y": (l.y_offset, torch.float32, (rows, self.intermediate_hidden)),
-            "h": (l.y_offset, torch.bfloat16, (rows, 2 * self.intermediate_hidden)),
+            "y16": (l.y_offset, torch.bfloat16, (rows, self.intermediate_hidden)),
             "act": (l.act_offset, torch.float8_e4m3fn, (rows, self.intermediate_hidden)),
             "part": (l.part_offset, torch.bfloat16, (rows, self.hidden)),
             "row_dest": (l.row_dest_offset, torch.int32, (rows,)),
