@@ -79,7 +79,33 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
     const int tok = direct ? r.dest.row_token[row] : 0;
     uint32_t* ar = reinterpret_cast<uint32_t*>(r.act + static_cast<int64_t>(row) * r.inter);
     float m = 0.0f;
-    if (groups <= kRequantGroups * kWave) {
+    if (kY16 && (r.inter & 7) == 0 && r.inter <= 8 * (kRequantGroups / 2) * kWave) {
+      // bf16 y: 8 channels (16 bytes) a load, their 8 codes one 8-byte store
+      const int octs = r.inter >> 3;
+      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(r.src) + static_cast<int64_t>(row) * r.inter);
+      float4 v[kRequantGroups];
+#pragma unroll
+      for (int j = 0; j < kRequantGroups / 2; ++j) {
+        const int o = lane + j * kWave;
+        const uint4 b = o < octs ? ld_nt(src + o) : make_uint4(0, 0, 0, 0);
+        v[2 * j] = make_float4(bf16_to_f32(b.x & 0xffff), bf16_to_f32(b.x >> 16), bf16_to_f32(b.y & 0xffff),
+                               bf16_to_f32(b.y >> 16));
+        v[2 * j + 1] = make_float4(bf16_to_f32(b.z & 0xffff), bf16_to_f32(b.z >> 16), bf16_to_f32(b.w & 0xffff),
+                                   bf16_to_f32(b.w >> 16));
+        m = abs_max4(abs_max4(m, v[2 * j]), v[2 * j + 1]);
+      }
+      m = wave_max(m);
+      const float inv = kE4m3Max / fmaxf(m, kAmaxFloor);
+      u32x2_t* dst = reinterpret_cast<u32x2_t*>(r.act + static_cast<int64_t>(row) * r.inter);
+#pragma unroll
+      for (int j = 0; j < kRequantGroups / 2; ++j) {
+        const int o = lane + j * kWave;
+        const float4 a = v[2 * j], c = v[2 * j + 1];
+        const u32x2_t codes = {pack_e4m3x4(a.x * inv, a.y * inv, a.z * inv, a.w * inv),
+                               pack_e4m3x4(c.x * inv, c.y * inv, c.z * inv, c.w * inv)};
+        if (o < octs) __builtin_nontemporal_store(codes, dst + o);
+      }
+    } else if (groups <= kRequantGroups * kWave) {
       float4 v[kRequantGroups];
 #pragma unroll
       for (int i = 0; i < kRequantGroups; ++i) {
