@@ -750,10 +750,15 @@ __device__ __forceinline__ void store_wide_swiglu(const GemmArgs& g, const v16f 
         const float4 wg = bs[0][q], wu = bs[1][q];
         const v16f& ag = acc[tm][0];
         const v16f& au = acc[tm][1];
-        const float y0 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q] * xs * wg.x), bf16_round(au[4 * q] * xs * wu.x), rw, cv);
-        const float y1 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q + 1] * xs * wg.y), bf16_round(au[4 * q + 1] * xs * wu.y), rw, cv);
-        const float y2 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q + 2] * xs * wg.z), bf16_round(au[4 * q + 2] * xs * wu.z), rw, cv);
-        const float y3 = swiglu_weighted_c<kClamp>(bf16_round(ag[4 * q + 3] * xs * wg.w), bf16_round(au[4 * q + 3] * xs * wu.w), rw, cv);
+        // gate and up of a channel rounded to bf16 together (one conversion for the pair)
+        auto y_of = [&](float a_g, float a_u, float w_g, float w_u) {
+          const uint32_t h = pack_bf16x2(a_g * xs * w_g, a_u * xs * w_u);
+          return swiglu_weighted_c<kClamp>(__uint_as_float(h << 16), __uint_as_float(h & 0xffff0000u), rw, cv);
+        };
+        const float y0 = y_of(ag[4 * q], au[4 * q], wg.x, wu.x);
+        const float y1 = y_of(ag[4 * q + 1], au[4 * q + 1], wg.y, wu.y);
+        const float y2 = y_of(ag[4 * q + 2], au[4 * q + 2], wg.z, wu.z);
+        const float y3 = y_of(ag[4 * q + 3], au[4 * q + 3], wg.w, wu.w);
         // channels 8q + 4hk .. +4 -> bytes 16q + 8hk of the row: piece q, half hk
         *reinterpret_cast<uint2*>(wlds + r * 64 + ((q ^ rkey) << 4) + hk * 8) =
             make_uint2(pack_bf16x2(y0, y1), pack_bf16x2(y2, y3));
