@@ -80,7 +80,7 @@ typedef struct mmoe_scratch_layout {
   int64_t counts_offset;       /* int32 [E]   rows per local expert */
   int64_t offsets_offset;      /* int32 [E+1] first row of each expert (exclusive scan) */
   int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R; [1] = 1: GEMM1 left
-                                  the bf16 pre-activation h in y's bytes; [2] = 1: GEMM2 wrote
+                                  y in bf16 ([R, I] in y's bytes); [2] = 1: GEMM2 wrote
                                   the rows of single-slot tokens straight to y (row_dest);
                                   [3] = the call's status (bounded waits of the decode pipeline
                                   that ran out; 0 = y is valid; MMOE_SCRATCH_STATUS_OFFSET);
@@ -217,10 +217,9 @@ int mmoe_forward_static(const mmoe_forward_args* args, void* stream);
 /* Stages of mmoe_forward, in order; each reads what the earlier ones left in route_scratch. */
 #define MMOE_STAGE_ROUTE 0   /* counts, offsets, output_index, per-row tables, stats */
 #define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I]; on the 4-wave
-                                kernel the bf16 pre-activation h [R, 2I] in y's bytes instead
-                                (meta[1] = 1) */
-#define MMOE_STAGE_REQUANT 2 /* (SwiGLU x weight of h first, when meta[1] = 1) row max |y| ->
-                                amax [R], act e4m3 [R, I], act_scale [R]; row_dest, meta[2] */
+                                kernel y in bf16 [R, I] instead (meta[1] = 1) */
+#define MMOE_STAGE_REQUANT 2 /* row max |y| -> amax [R], act e4m3 [R, I], act_scale [R];
+                                row_dest, meta[2] */
 #define MMOE_STAGE_GEMM2 3   /* part bf16 [R, H]; with meta[2] = 1 the rows of single-slot
                                 tokens go straight to y */
 #define MMOE_STAGE_COMBINE 4 /* y (tokens written by GEMM2 are left as they are) */
