@@ -145,7 +145,12 @@ def _stage_checks(buf, tr, s, clamp=None):
     act = buf.scratch_view("act")[:r].cpu()
     deq = act.float() * act_s.view(-1, 1)
     deq_ref = tr.act.float() * tr.act_scale.view(-1, 1)
-    assert O.calc_diff(deq, deq_ref) < 1e-4, "SwiGLU requant"
+    # The oracle quantizes f32 y. bf16 y (the WIDE GEMM1's, the reference fused path's rounding)
+    # moves a code by one e4m3 step wherever its rounding crosses a code boundary: about one
+    # element in 60 (bf16 keeps 5 more mantissa bits than e4m3), at ~6% each.
+    d_act = O.calc_diff(deq, deq_ref)
+    log(f"  requant: calc_diff(act) = {d_act:.2e} ({'bf16' if y16 else 'f32'} y)")
+    assert d_act < (5e-4 if y16 else 1e-4), "SwiGLU requant"
     part = buf.scratch_view("part")[:r].cpu()
     if buf.scratch_view("meta")[2].item() == 1:
         # GEMM2 wrote the rows of single-slot tokens straight to y: row_dest names exactly those
