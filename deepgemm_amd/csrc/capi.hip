@@ -65,7 +65,7 @@ void plan_scratch(int num_ranks, int num_experts, int num_max_tokens, int num_to
   l->m_indices_offset = take(rows * 4);
   l->act_scale_offset = take(rows * 4);
   l->amax_offset = take(rows * 4);
-  l->y_offset = take(rows * static_cast<int64_t>(intermediate) * 4);
+  l->y_offset = take(rows * static_cast<int64_t>(intermediate) * 2);
   l->act_offset = take(rows * static_cast<int64_t>(intermediate));
   l->part_offset = take(rows * static_cast<int64_t>(hidden) * 2);
   l->row_dest_offset = take(rows * 4);
@@ -377,7 +377,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
   g1.sw.enabled = 1;
   g1.sw.inter = a->intermediate;
   g1.sw.row_weight = at<float>(ws, l.row_weight_offset);
-  g1.sw.y = at<float>(ws, l.y_offset);
+  g1.sw.y = at<uint16_t>(ws, l.y_offset);
   g1.sw.has_clamp = isfinite(a->activation_clamp) ? 1 : 0;
   g1.sw.clamp = a->activation_clamp;
   g1.sched = at<int32_t>(ws, l.sched_offset);
@@ -479,7 +479,7 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     const bool dual1 = wide1 && dual_rows != nullptr;
     mark_stage(MMOE_STAGE_REQUANT);
     if (runs(MMOE_STAGE_REQUANT) &&
-        mmoe::launch_requant(at<float>(ws, l.y_offset), wide1, at<float>(ws, l.amax_offset),
+        mmoe::launch_requant(at<uint16_t>(ws, l.y_offset), wide1, at<float>(ws, l.amax_offset),
                              at<int32_t>(ws, l.meta_offset), at<uint8_t>(ws, l.act_offset),
                              at<float>(ws, l.act_scale_offset), max_rows, a->intermediate, dest,
                              cus, s, dual1 ? dual_rows : nullptr, dual_min) != hipSuccess)

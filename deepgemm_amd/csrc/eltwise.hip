@@ -20,19 +20,19 @@ constexpr int kEltWaves = kEltThreads / kWave;
 // act_scale = a/448 (the K2 requant, megamoe/dcu_megamoe_large_opt/K2_fused/
 // k2_fused_ext.cu:341-364). A row of up to kRequantGroups*4*64 channels stays in registers
 // between the reduction and the quantization; a longer one is read twice. y is GEMM1's SwiGLU
-// x route weight output (k2_fused_ext.cu:283-340, computed in GEMM1's epilogue): f32 from the
-// 8-wave kernels, bf16 from the WIDE kernel (kY16).
+// x route weight output in bf16 (k2_fused_ext.cu:283-340, computed in GEMM1's epilogue and
+// rounded as the reference's fused path rounds its activation, mega_moe_dcu_tiles.cuh:530-550).
 constexpr int kRequantGroups = 8;  // float4 groups per lane held in registers
 
 struct RequantArgs {
-  const void* src;  // f32 y [rows, I], or bf16 y [rows, I] (kY16)
+  const uint16_t* src;  // bf16 y [rows, I]
   float* amax;
   int32_t* meta;
   uint8_t* act;
   float* act_scale;
   int inter;
   RowDest dest;
-  const int32_t* dual_rows;  // dual launches: bf16 y iff *dual_rows >= dual_min_rows
+  const int32_t* dual_rows;  // dual launches: the WIDE GEMM1 ran iff *dual_rows >= dual_min_rows
   int dual_min_rows;
 };
 
@@ -57,32 +57,30 @@ __device__ __forceinline__ uint4 ld_nt(const uint4* p) {
 }
 
 // channels 4q .. 4q+3 of row `row`
-template <bool kY16>
 __device__ __forceinline__ float4 requant_load(const RequantArgs& r, int64_t row, int q) {
-  if (!kY16) return ld_nt(reinterpret_cast<const float4*>(static_cast<const float*>(r.src) + row * r.inter) + q);
-  const uint2 b = ld_nt(reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(r.src) + row * r.inter) + q);
+  const uint2 b = ld_nt(reinterpret_cast<const uint2*>(r.src + row * r.inter) + q);
   return make_float4(bf16_to_f32(b.x & 0xffff), bf16_to_f32(b.x >> 16), bf16_to_f32(b.y & 0xffff),
                      bf16_to_f32(b.y >> 16));
 }
 
-template <bool kY16>
-__device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) {
+// wide: the WIDE GEMM1 ran (meta[1]); direct: build the direct-write table
+__device__ __forceinline__ void requant_rows(const RequantArgs& r, bool wide, bool direct) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int rows = r.meta[0];
   const int groups = r.inter >> 2;
   if (blockIdx.x == 0 && threadIdx.x == 0) {
-    r.meta[1] = kY16 ? 1 : 0;
+    r.meta[1] = wide ? 1 : 0;
     if (r.dest.meta_flag != nullptr) *r.dest.meta_flag = direct ? 1 : 0;
   }
   for (int row = blockIdx.x * kEltWaves + wave; row < rows; row += gridDim.x * kEltWaves) {
     const int tok = direct ? r.dest.row_token[row] : 0;
     uint32_t* ar = reinterpret_cast<uint32_t*>(r.act + static_cast<int64_t>(row) * r.inter);
     float m = 0.0f;
-    if (kY16 && (r.inter & 7) == 0 && r.inter <= 8 * (kRequantGroups / 2) * kWave) {
-      // bf16 y: 8 channels (16 bytes) a load, their 8 codes one 8-byte store
+    if ((r.inter & 7) == 0 && r.inter <= 8 * (kRequantGroups / 2) * kWave) {
+      // 8 channels (16 bytes) a load, their 8 codes one 8-byte store
       const int octs = r.inter >> 3;
-      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(r.src) + static_cast<int64_t>(row) * r.inter);
+      const uint4* src = reinterpret_cast<const uint4*>(r.src + static_cast<int64_t>(row) * r.inter);
       float4 v[kRequantGroups];
 #pragma unroll
       for (int j = 0; j < kRequantGroups / 2; ++j) {
@@ -110,7 +108,7 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
 #pragma unroll
       for (int i = 0; i < kRequantGroups; ++i) {
         const int q = lane + i * kWave;
-        v[i] = q < groups ? requant_load<kY16>(r, row, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[i] = q < groups ? requant_load(r, row, q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         m = abs_max4(m, v[i]);
       }
       m = wave_max(m);
@@ -121,11 +119,11 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
         if (q < groups) __builtin_nontemporal_store(pack_e4m3x4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv), ar + q);
       }
     } else {
-      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, requant_load<kY16>(r, row, q));
+      for (int q = lane; q < groups; q += kWave) m = abs_max4(m, requant_load(r, row, q));
       m = wave_max(m);
       const float inv = kE4m3Max / fmaxf(m, kAmaxFloor);
       for (int q = lane; q < groups; q += kWave) {
-        const float4 v = requant_load<kY16>(r, row, q);
+        const float4 v = requant_load(r, row, q);
         __builtin_nontemporal_store(pack_e4m3x4(v.x * inv, v.y * inv, v.z * inv, v.w * inv), ar + q);
       }
     }
@@ -143,15 +141,14 @@ __device__ __forceinline__ void requant_rows(const RequantArgs& r, bool direct) 
   }
 }
 
-// kMode 0: from f32 y, 1: from bf16 y, 2: decided on the device (a dual GEMM1 launch;
-// RequantArgs)
+// kMode 0: after the 8-wave GEMM1, 1: after the WIDE GEMM1, 2: decided on the device (a dual
+// GEMM1 launch; RequantArgs)
 template <int kMode>
 __global__ __launch_bounds__(kEltThreads) void requant_kernel(RequantArgs r) {
-  // (after a dual launch the direct rows go with the WIDE GEMMs only: bf16 y)
-  const bool y16 = kMode == 1 || (kMode == 2 && *r.dual_rows >= r.dual_min_rows);
-  const bool direct = r.dest.row_dest != nullptr && (kMode != 2 || y16);
-  if (y16) requant_rows<true>(r, direct);
-  else requant_rows<false>(r, direct);
+  // (after a dual launch the direct rows go with the WIDE GEMMs only)
+  const bool wide = kMode == 1 || (kMode == 2 && *r.dual_rows >= r.dual_min_rows);
+  const bool direct = r.dest.row_dest != nullptr && (kMode != 2 || wide);
+  requant_rows(r, wide, direct);
 }
 
 // ---------------------------------------------------------------- combine
@@ -366,7 +363,7 @@ unsigned grid_for(int64_t work_items, int64_t per_block, int64_t cap) {
 
 }  // namespace
 
-hipError_t launch_requant(const void* src, bool y16, float* amax, int32_t* meta, uint8_t* act,
+hipError_t launch_requant(const uint16_t* src, bool wide, float* amax, int32_t* meta, uint8_t* act,
                           float* act_scale, int64_t max_rows, int inter, const RowDest& dest,
                           int num_cus, hipStream_t stream, const int32_t* dual_rows,
                           int dual_min_rows) {
@@ -381,7 +378,7 @@ hipError_t launch_requant(const void* src, bool y16, float* amax, int32_t* meta,
   const unsigned grid = grid_for(max_rows, kEltWaves, static_cast<int64_t>(num_cus) * 16);
   if (dual_rows != nullptr)
     return launch_kernel(requant_kernel<2>, dim3(grid), dim3(kEltThreads), 0, stream, r);
-  if (y16) return launch_kernel(requant_kernel<1>, dim3(grid), dim3(kEltThreads), 0, stream, r);
+  if (wide) return launch_kernel(requant_kernel<1>, dim3(grid), dim3(kEltThreads), 0, stream, r);
   return launch_kernel(requant_kernel<0>, dim3(grid), dim3(kEltThreads), 0, stream, r);
 }
 

@@ -199,9 +199,12 @@ __device__ __forceinline__ void publish_tile_scales(TileTables& tt, const TileSc
 // of the output (SwiGLU: 32 channels).
 // kCoherent: the stores go out device-coherent (sc1, written through the XCD's L2): GEMM2's
 // partial rows, so that workgroups of other XCDs can read them in the same launch, and GEMM1's
-// fp32 SwiGLU rows of the decode pipeline, which its GEMM2 items of the same XCD still read from
-// L2 but which no longer sit there dirty (c1 150.9 -> 148.9 us per layer; its y output rows
-// written through as well made no difference, its act rows as 4-byte coherent stores +3 us).
+// SwiGLU rows of the decode pipeline, which its GEMM2 items of the same XCD still read from L2
+// but which no longer sit there dirty (c1 150.9 -> 148.9 us per layer; its y output rows written
+// through as well made no difference, its act rows as 4-byte coherent stores +3 us).
+// SwiGLU: y is stored in bf16 (the reference fused path's rounding of the activation before
+// its quantization). kPmax (the decode pipeline's GEMM1): the row maxima of the rounded values
+// are stored as well.
 template <bool kSwiglu, int MT, bool kPmax = false, bool kCoherent = false>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[MT][2], int row0,
                                            int mrows, int unit, const TileTables& tt, int trow0) {
@@ -238,12 +241,13 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const v16f (&acc)[
         }
       } else {
         const float yv = swiglu_value(g, acc[mt][0][v], acc[mt][1][v], xs[v], b0, b1, rw[v]);
+        const int64_t at = static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl;
+        const uint16_t yb = f32_to_bf16(yv);
         if constexpr (kCoherent)
-          __hip_atomic_store(&g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl], yv,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(g.sw.y + at, yb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         else
-          g.sw.y[static_cast<int64_t>(row0 + r) * g.sw.inter + unit * 32 + rl] = yv;
-        pm[v] = fabsf(yv);
+          g.sw.y[at] = yb;
+        if constexpr (kPmax) pm[v] = fabsf(bf16_to_f32(yb));
       }
     }
     if constexpr (kPmax && kSwiglu) {
@@ -734,7 +738,7 @@ __device__ __forceinline__ void store_wide_swiglu(const GemmArgs& g, const v16f 
     for (int q = 0; q < 4; ++q) bs[tn][q] = *reinterpret_cast<const float4*>(s_bs + tn * 32 + q * 8 + hk * 4);
   uint8_t* wlds = stage + (tid / kWave) * 4096;
   const int64_t ld = g.sw.inter;
-  uint16_t* out = reinterpret_cast<uint16_t*>(g.sw.y) + static_cast<int64_t>(row0) * ld + unit * 32 + (lane & 3) * 8;
+  uint16_t* out = g.sw.y + static_cast<int64_t>(row0) * ld + unit * 32 + (lane & 3) * 8;
   const float cv = g.sw.clamp;
 #pragma unroll
   for (int pass = 0; pass < (TM + 1) / 2; ++pass) {
@@ -1483,7 +1487,7 @@ __device__ void plan_groups(int E, const int* s_count, int* s_gprefix) {
   if (lane == 0) s_gprefix[E] = carry;
 }
 
-// The requant of rows [row0, row0 + mrows) of GEMM1's fp32 output y into the LDS A chunk buffers
+// The requant of rows [row0, row0 + mrows) of GEMM1's bf16 output y into the LDS A chunk buffers
 // of a STREAM GEMM2 tile of MT 32-row tiles (stream_tile's chunk layout; K = I in one chunk for
 // MT = 1, two for MT = 2): the row's amax, inv = 448 / max(amax, 1e-4), then 16 e4m3 codes per
 // LDS piece -- the requant kernel's arithmetic, so the same bits. The amax is the max of the
@@ -1505,7 +1509,7 @@ __device__ void stage_rows_from_y(const PipeArgs& p, int row0, int mrows, bool w
   const int nchunks = inter / kc;
   const int tid = opaque_tid();
   const int lane = tid & (kWave - 1), wave = tid / kWave;
-  const float* y = p.g1.sw.y;
+  const uint16_t* y = p.g1.sw.y;
   const int r8 = tid >> 3;
   float4 pm[kUnits / 32];
 #pragma unroll
@@ -1517,8 +1521,9 @@ __device__ void stage_rows_from_y(const PipeArgs& p, int row0, int mrows, bool w
     for (int j = 0; j < kUnits / 32; ++j) pm[j] = src[j];
   }
   // batch b of chunk c: pieces i = b * kStageBatch + h; piece i of a lane holds LDS bytes
-  // (i * 8 + wave) * 1024 + lane * 16 of the chunk buffer (row r, swizzled piece)
-  float4 v[kStageBatch][4];
+  // (i * 8 + wave) * 1024 + lane * 16 of the chunk buffer (row r, swizzled piece): 16 channels,
+  // 32 bytes of y
+  uint4 v[kStageBatch][2];
   auto load_batch = [&](int c, int b) {
 #pragma unroll
     for (int h = 0; h < kStageBatch; ++h) {
@@ -1526,12 +1531,14 @@ __device__ void stage_rows_from_y(const PipeArgs& p, int row0, int mrows, bool w
       const int r = pos / kc;
       const int off = c * kc + swizzle_piece((pos - r * kc) >> 4, r) * 16;
       if (r < mrows) {
-        const float4* src = reinterpret_cast<const float4*>(y + static_cast<int64_t>(row0 + r) * inter + off);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[h][j] = src[j];
+        const uint4* src = reinterpret_cast<const uint4*>(y + static_cast<int64_t>(row0 + r) * inter + off);
+        v[h][0] = src[0];
+        v[h][1] = src[1];
       }
     }
   };
+  auto lo = [](uint32_t w) { return bf16_to_f32(static_cast<uint16_t>(w & 0xffff)); };
+  auto hi = [](uint32_t w) { return bf16_to_f32(static_cast<uint16_t>(w >> 16)); };
   load_batch(0, 0);
   {
     float m = 0.0f;
@@ -1560,10 +1567,11 @@ __device__ void stage_rows_from_y(const PipeArgs& p, int row0, int mrows, bool w
         int4 q = make_int4(0, 0, 0, 0);  // rows past mrows: never stored
         if (r < mrows) {
           const float inv = s_inv[r];
-          q.x = static_cast<int>(pack_e4m3x4(v[h][0].x * inv, v[h][0].y * inv, v[h][0].z * inv, v[h][0].w * inv));
-          q.y = static_cast<int>(pack_e4m3x4(v[h][1].x * inv, v[h][1].y * inv, v[h][1].z * inv, v[h][1].w * inv));
-          q.z = static_cast<int>(pack_e4m3x4(v[h][2].x * inv, v[h][2].y * inv, v[h][2].z * inv, v[h][2].w * inv));
-          q.w = static_cast<int>(pack_e4m3x4(v[h][3].x * inv, v[h][3].y * inv, v[h][3].z * inv, v[h][3].w * inv));
+          const uint4 a = v[h][0], b2 = v[h][1];
+          q.x = static_cast<int>(pack_e4m3x4(lo(a.x) * inv, hi(a.x) * inv, lo(a.y) * inv, hi(a.y) * inv));
+          q.y = static_cast<int>(pack_e4m3x4(lo(a.z) * inv, hi(a.z) * inv, lo(a.w) * inv, hi(a.w) * inv));
+          q.z = static_cast<int>(pack_e4m3x4(lo(b2.x) * inv, hi(b2.x) * inv, lo(b2.y) * inv, hi(b2.y) * inv));
+          q.w = static_cast<int>(pack_e4m3x4(lo(b2.z) * inv, hi(b2.z) * inv, lo(b2.w) * inv, hi(b2.w) * inv));
           if (write_act) {
             const int off = c * kc + swizzle_piece((pos - r * kc) >> 4, r) * 16;
             *reinterpret_cast<int4*>(p.act + static_cast<int64_t>(row0 + r) * inter + off) = q;
@@ -1623,7 +1631,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void decode_pipeline_kernel(PipeAr
     }
     if (threadIdx.x == 0) {
       ra.meta[0] = s_off[E] < ra.row_cap ? s_off[E] : static_cast<int>(ra.row_cap);
-      p.meta[1] = 0;  // the requant read GEMM1's y
+      p.meta[1] = 0;  // the 8-wave GEMM1
       if (p.direct_flag != nullptr) *p.direct_flag = 0;
       if (hw >= kPipeXcds) atomicAdd(&p.pipe[kPipeFailAt], 1);  // an XCD id this launch does not expect
     }

@@ -56,8 +56,7 @@ struct SwigluEpilogue {
   int enabled;
   int inter;                // I: gate weight rows [0, I), up rows [I, 2I)
   const float* row_weight;  // [rows] top-k weight of each routed row
-  float* y;                 // f32 [rows, I] SwiGLU output (before requant), or with the WIDE
-                            // kernel bf16 [rows, I] (gemm_wide_selected)
+  uint16_t* y;              // bf16 [rows, I] SwiGLU x weight output (before the requant)
   int has_clamp;
   float clamp;
 };
@@ -163,12 +162,11 @@ struct RowDest {
 
 // Per-row requant of the SwiGLU output: amax = max |y| (written out), a = max(amax, 1e-4);
 // act = e4m3(clip(y * 448/a)); act_scale = a/448 -- for rows < meta[0]. y is GEMM1's SwiGLU x
-// route weight output [rows, I]: f32, or bf16 with y16 (the WIDE GEMM1's). meta[1] records
-// which (1 = bf16). With dest.row_dest it also builds the direct-write table (RowDest).
-// With dual_rows (a dual GEMM1 launch): y16 is decided on the device, true when
-// *dual_rows >= dual_min_rows (the WIDE GEMM1 ran), and the direct-write table is built only
-// then.
-hipError_t launch_requant(const void* src, bool y16, float* amax, int32_t* meta, uint8_t* act,
+// route weight output, bf16 [rows, I]. meta[1] records whether the WIDE GEMM1 ran (wide). With
+// dest.row_dest it also builds the direct-write table (RowDest). With dual_rows (a dual GEMM1
+// launch): wide is decided on the device, true when *dual_rows >= dual_min_rows, and the
+// direct-write table is built only then.
+hipError_t launch_requant(const uint16_t* src, bool wide, float* amax, int32_t* meta, uint8_t* act,
                           float* act_scale, int64_t max_rows, int inter, const RowDest& dest,
                           int num_cus, hipStream_t stream, const int32_t* dual_rows = nullptr,
                           int dual_min_rows = 0);

@@ -278,12 +278,12 @@ class SymmBuffer:
     def scratch_view(self, name: str, num_rows: Optional[int] = None) -> torch.Tensor:
         """Intermediate tensors of the last call: counts, offsets, meta, output_index,
         row_token, row_weight, m_indices, act_scale, amax (max |y| per row), y (SwiGLU x
-        weight, f32), act (requantised y), part (GEMM2 rows), row_dest (the token whose y
+        weight, bf16), act (requantised y), part (GEMM2 rows), row_dest (the token whose y
         row GEMM2 wrote directly for a row, else -1; built in calls with the WIDE GEMMs, where
         those rows' part is not written; meta[2] == 1 then), sched and pipe (the GEMMs' work
         counters, zero between calls), pmax (per row, max |y| of each 64-column block of GEMM1's
-        output; written by the one-launch decode pipeline only). When meta[1] == 1 the GEMM1 of
-        the call (the WIDE kernel) left y in bf16, in the same bytes: view it as y16."""
+        output; written by the one-launch decode pipeline only). meta[1] == 1 when GEMM1 ran on
+        the WIDE kernel."""
         l = self.scratch_layout
         e, t, k = self.num_experts, self.num_max_tokens_per_rank, self.num_topk
         rows = int(l.row_capacity if num_rows is None else num_rows)
@@ -297,8 +297,7 @@ class SymmBuffer:
             "m_indices": (l.m_indices_offset, torch.int32, (rows,)),
             "act_scale": (l.act_scale_offset, torch.float32, (rows,)),
             "amax": (l.amax_offset, torch.float32, (rows,)),
-            "y": (l.y_offset, torch.float32, (rows, self.intermediate_hidden)),
-            "y16": (l.y_offset, torch.bfloat16, (rows, self.intermediate_hidden)),
+            "y": (l.y_offset, torch.bfloat16, (rows, self.intermediate_hidden)),
             "act": (l.act_offset, torch.float8_e4m3fn, (rows, self.intermediate_hidden)),
             "part": (l.part_offset, torch.bfloat16, (rows, self.hidden)),
             "row_dest": (l.row_dest_offset, torch.int32, (rows,)),

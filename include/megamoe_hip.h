@@ -79,8 +79,8 @@ typedef struct mmoe_scratch_layout {
   int64_t num_chunks;          /* routing chunks of MMOE_ROUTE_CHUNK tasks */
   int64_t counts_offset;       /* int32 [E]   rows per local expert */
   int64_t offsets_offset;      /* int32 [E+1] first row of each expert (exclusive scan) */
-  int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R; [1] = 1: GEMM1 left
-                                  y in bf16 ([R, I] in y's bytes); [2] = 1: GEMM2 wrote
+  int64_t meta_offset;         /* int32 [16]  [0] = total routed rows R; [1] = 1: GEMM1 ran on
+                                  the WIDE kernel; [2] = 1: GEMM2 wrote
                                   the rows of single-slot tokens straight to y (row_dest);
                                   [3] = the call's status (bounded waits of the decode pipeline
                                   that ran out; 0 = y is valid; MMOE_SCRATCH_STATUS_OFFSET);
@@ -93,7 +93,7 @@ typedef struct mmoe_scratch_layout {
   int64_t m_indices_offset;    /* int32 [rows] local expert of each routed row */
   int64_t act_scale_offset;    /* f32   [rows] per-row FP8 scale of the SwiGLU output */
   int64_t amax_offset;         /* f32   [rows] max |y| per row (written by the requant stage) */
-  int64_t y_offset;            /* f32   [rows, I]  SwiGLU x weight output of GEMM1 */
+  int64_t y_offset;            /* bf16  [rows, I]  SwiGLU x weight output of GEMM1 */
   int64_t act_offset;          /* e4m3  [rows, I]  requantised SwiGLU output */
   int64_t part_offset;         /* bf16  [rows, H]  per-row GEMM2 output (combine partials);
                                   in a prefill call (WIDE GEMMs) the rows of tokens with a
@@ -216,8 +216,7 @@ int mmoe_forward_static(const mmoe_forward_args* args, void* stream);
 
 /* Stages of mmoe_forward, in order; each reads what the earlier ones left in route_scratch. */
 #define MMOE_STAGE_ROUTE 0   /* counts, offsets, output_index, per-row tables, stats */
-#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y f32 [R, I]; on the 4-wave
-                                kernel y in bf16 [R, I] instead (meta[1] = 1) */
+#define MMOE_STAGE_GEMM1 1   /* gate||up GEMM + SwiGLU x weight -> y bf16 [R, I] */
 #define MMOE_STAGE_REQUANT 2 /* row max |y| -> amax [R], act e4m3 [R, I], act_scale [R];
                                 row_dest, meta[2] */
 #define MMOE_STAGE_GEMM2 3   /* part bf16 [R, H]; with meta[2] = 1 the rows of single-slot
