@@ -473,8 +473,8 @@ int mmoe_forward_stages(const mmoe_forward_args* a, int first_stage, int last_st
     if (runs(MMOE_STAGE_GEMM1) &&
         mmoe::launch_grouped_gemm(g1, max_rows, cus, s, dual_rows, route_small_in_gemm1, dual_min) != hipSuccess)
       return MMOE_ERR_HIP;
-    // the WIDE GEMM1 leaves bf16 y, the 8-wave one f32 y (after a dual GEMM1 launch the requant
-    // finds out on the device which GEMM1 ran)
+    // (after a dual GEMM1 launch the requant finds out on the device which GEMM1 ran: the
+    // direct-write table goes with the WIDE GEMMs only)
     const bool wide1 = mmoe::gemm_wide_selected(g1, max_rows);
     const bool dual1 = wide1 && dual_rows != nullptr;
     mark_stage(MMOE_STAGE_REQUANT);

@@ -1351,7 +1351,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
 // claim goes out one item ahead, so its latency hides behind an item.
 //
 // Hand-off, inside the XCD, whose CUs share its L2 (the per-CU L1 is write-through): a GEMM1
-// item waits for its fp32 SwiGLU stores (vmcnt 0) and counts itself done for its group. A GEMM2
+// item waits for its bf16 SwiGLU stores (vmcnt 0) and counts itself done for its group. A GEMM2
 // item issues its first weight steps, polls until its group's count is complete, invalidates
 // its CU's L1 and requantizes the group's rows from L2 straight into its LDS A buffers (the
 // requant kernel's arithmetic, so the same bits; the group's first GEMM2 item also writes act

@@ -51,7 +51,7 @@ inline int64_t route_count_ints(int64_t max_tasks, int num_experts) {
 // (weight streaming, decode) and TILE otherwise (256x256 MFMA tiles, prefill).
 enum class GemmEngine : int { kAuto = 0, kStream = 1, kTile = 2 };
 
-// Fused GEMM1 epilogue: SwiGLU x route weight -> fp32 y.
+// Fused GEMM1 epilogue: SwiGLU x route weight -> bf16 y.
 struct SwigluEpilogue {
   int enabled;
   int inter;                // I: gate weight rows [0, I), up rows [I, 2I)
@@ -141,8 +141,8 @@ int gemm_wide_min_rows(int num_experts);
 bool gemm_eager_dual(const GemmArgs& g, int max_rows);
 int gemm_eager_dual_min_largest();
 bool gemm_shape_supported(int n, int k);
-// True when launch_grouped_gemm runs the WIDE kernel for g: GEMM1 then writes the bf16
-// pre-activation h [rows, 2I] instead of the SwiGLU output y (requant computes the SwiGLU).
+// True when launch_grouped_gemm runs the WIDE kernel for g (the choice depends only on the
+// shape and the row bound, so separate stage calls agree on it).
 bool gemm_wide_selected(const GemmArgs& g, int max_rows);
 // Largest task count (S*K) and expert count GEMM1 can route in-kernel.
 int gemm_route_max_tasks();
@@ -219,7 +219,7 @@ constexpr int kPipeDone2At = kPipeHeader + kMaxPipeGroups;
 constexpr int kPipeDone2Stride = 16;
 constexpr int kPipeInts = kPipeHeader + kMaxPipeGroups + kMaxPipeExperts * kPipeDone2Stride;
 struct PipeArgs {
-  GemmArgs g1;           // GEMM1: route_in_kernel 1, SwiGLU epilogue into the fp32 y
+  GemmArgs g1;           // GEMM1: route_in_kernel 1, SwiGLU epilogue into the bf16 y
   GemmArgs g2;           // GEMM2: a = act, a_scale = act_scale, c = the bf16 partial rows
   uint8_t* act;          // e4m3 [rows, I] (written by the first GEMM2 item of each group)
   float* act_scale;      // [rows]

@@ -607,8 +607,8 @@ def test_decode_pipeline_many_experts(mm, cuda, e, s, g):
 
 def test_caller_scratch_reused_across_shapes(mm, cuda, full_weights):
     """One caller-owned route_scratch, zero-filled once, serves mmoe_forward calls of different
-    shapes in turn through the C ABI: an all-local 1024-token call (6144 rows: its fp32 y spans
-    50 MB), a 200-token call, an all-local 4096-token prefill call (the WIDE kernels), and the
+    shapes in turn through the C ABI: an all-local 1024-token call (6144 rows: its y spans
+    25 MB), a 200-token call, an all-local 4096-token prefill call (the WIDE kernels), and the
     first call again. Each is bitwise equal to the same call on a fresh zero-filled scratch and
     reports status 0, and the decode pipeline's counters read zero after each: they sit at
     offset 0 in every layout, and every call leaves them zero."""

@@ -48,9 +48,10 @@ def test_static_scratch_matches_mmoe_forward(mm, cuda):
     e, hdim, inter, k = 32, 4096, 2048, 6
     l1, l2 = make_weights_gpu(e, hdim, inter, seed=4321, mm=mm)
     # call 1: the decode config's size (1024 tokens, capacity 1152); call 2: the same capacity
-    # with every slot local (6144 rows: its fp32 y alone spans 50 MB of the static array); call 3:
-    # a smaller input, whose own layout would have put the pipeline counters inside call 2's y
-    # region had they not sat at offset 0 in every layout
+    # with every slot local (6144 rows: its y alone spans 25 MB of the static array); call 3:
+    # a smaller input with a layout of its own, whose sections sit where call 2's y and partial
+    # rows were (its pipeline counters start at zero only because they sit at offset 0 in every
+    # layout and each call leaves them zero)
     for s, g, clamp in ((1024, 256, None), (1024, None, None), (200, 64, 1.0)):
         log(f"static scratch: S={s} clamp={clamp}")
         x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=77 + s, global_experts=g)
