@@ -206,7 +206,7 @@ int mmoe_scratch_status(const void* route_scratch, int32_t* out, void* stream);
  * args->route_scratch and args->route_scratch_bytes are ignored. The scratch is instead a
  * static device array of MMOE_STATIC_SCRATCH_BYTES that the library holds on each GPU it runs
  * on until the process ends: calls whose mmoe_route_scratch_bytes() (for their num_max_tokens)
- * exceeds it return MMOE_ERR_STATIC_SCRATCH (128 MiB covers a token capacity of 1152 at
+ * exceeds it return MMOE_ERR_STATIC_SCRATCH (128 MiB covers a token capacity of 1488 at
  * E = 32, H = 4096, I = 2048, top-6). Nothing is allocated on any call (no hipMalloc, no
  * hipFree, no allocating library routine). Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (other streams, other host threads) race and must be
