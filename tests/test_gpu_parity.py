@@ -217,6 +217,43 @@ def test_layer_small_shapes(mm, cuda, cfg):
     assert d <= CALC_DIFF_BAR
 
 
+# other models' expert shapes, one GPU's EP share of 32 experts: (S, H, I, top-k, global
+# experts or None for all local). H = 7168 keeps GEMM1's K off the decode pipeline's 2048-byte
+# chunks (the 8-wave kernels with in-kernel routing run at decode); I = 1536 keeps GEMM2's K off
+# it; the prefill sizes run the WIDE kernels.
+OTHER_MODEL_CASES = {
+    "h7168_top8_decode": (512, 7168, 2048, 8, 256),
+    "h7168_top8_prefill": (1536, 7168, 2048, 8, None),
+    "i1536_top8_decode": (1024, 4096, 1536, 8, 128),
+    "i1536_top8_prefill": (1536, 4096, 1536, 8, None),
+}
+
+
+@pytest.mark.parametrize("case", list(OTHER_MODEL_CASES))
+def test_layer_other_model_shapes(mm, cuda, case):
+    """The layer at other MoE models' expert shapes (a DeepSeek-like hidden size of 7168 with
+    top-8, a Qwen-like expert width of 1536 with top-8): every stage against the oracle, the
+    combine bitwise, and the output within the bar, at a decode and a prefill size."""
+    s, hdim, inter, k, g = OTHER_MODEL_CASES[case]
+    e = 32
+    log(f"layer other-model case={case}")
+    x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=4242 + s + hdim, global_experts=g)
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=777 + inter, mm=mm)
+    buf = mm.get_symm_buffer_for_mega_moe(None, e, s, k, hdim, inter)
+    y = run_layer(mm, buf, x_fp8, x_sf, idx, w, l1, l2)
+    torch.cuda.synchronize()
+    l1c, l2c = cpu_weights(l1, l2)
+    tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c)
+    wide = s * k > 8192 and s * k >= 256 * e
+    assert (buf.scratch_view("meta")[1].item() == 1) == wide
+    _stage_checks(buf, tr, s, None)
+    _combine_bitwise(mm, buf, y, l1, l2, s, None)
+    d = O.calc_diff(y.cpu(), tr.y)
+    log(f"  R={tr.routing.num_rows} calc_diff={d:.3e}")
+    assert d <= CALC_DIFF_BAR
+    del l1, l2, l1c, l2c
+
+
 @pytest.fixture(scope="module")
 def full_weights(mm):
     """Full-shape weights (32 experts, H=4096, I=2048), drawn on the GPU, plus CPU copies."""
