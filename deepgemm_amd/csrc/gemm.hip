@@ -24,7 +24,8 @@
 // Two persistent kernels per GEMM; the host picks one (gemm_wide_selected):
 //  * the 8-wave kernel (one workgroup per CU) runs two tile engines, each expert's chosen on
 //    the device from its routed row count, and can route the tasks itself (decode sizes):
-//    - STREAM engine (<= 64 rows: decode, HBM-bound on the weights). A workgroup tile is
+//    - STREAM engine (<= 128 rows on the auto schedule: decode, HBM-bound on the weights;
+//      an expert with more than 64 rows is two row chunks). A workgroup tile is
 //      (expert, 512 output columns, <= 64 rows) over the full K; wave w owns columns
 //      [64w, 64w + 64) and streams its weight columns from global memory into a register ring
 //      4 steps deep (Marlin gives each lane 16 contiguous k-bytes of one weight row; 16 lanes
@@ -58,7 +59,8 @@ constexpr int kGemmWaves = kGemmThreads / kWave;
 constexpr int kMaxGemmExperts = 256;
 // STREAM engine
 constexpr int kStreamUnit = 64;     // output columns per wave
-constexpr int kStreamRows = 64;     // rows per workgroup tile (experts up to this many use it)
+constexpr int kStreamRows = 64;     // rows per workgroup tile
+constexpr int kStreamAutoMaxRows = 128;  // the auto schedule streams experts up to this many rows
 constexpr int kStreamDepth = 4;     // 64-k weight steps in flight per wave
 constexpr int kAChunk = 65536;      // bytes of one A chunk buffer (32*MT rows x 2048/MT k)
 constexpr int kALoads = kAChunk / 1024 / kGemmWaves;  // 16-byte A loads per lane per chunk
@@ -1121,7 +1123,7 @@ __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const 
       if (e < E) {
         const int cnt = s_count[e];
         const bool tile = all_tile || g.engine == GemmEngine::kTile ||
-                          (g.engine == GemmEngine::kAuto && cnt > kStreamRows);
+                          (g.engine == GemmEngine::kAuto && cnt > kStreamAutoMaxRows);
         items = tile ? (cnt + tile_rows - 1) / tile_rows * tile_nb
                      : (cnt + kStreamRows - 1) / kStreamRows * stream_nb;
         s_tile[e] = tile;
@@ -1971,17 +1973,18 @@ int gemm_wide_min_rows(int num_experts) {
 // Eager calls whose row bound selects WIDE only by a small margin: the routed rows may be far
 // fewer (an EP share keeps ~1/8 of its slots), so both kernels go out and the routing's largest
 // expert row count chooses on the device -- the 8-wave kernels while every expert has at most
-// 64 rows (each expert's weights streamed once by the STREAM engine), WIDE from 65 (the
-// STREAM engine would stream some experts' weights twice). Measured on the 8-wave kernels at
-// T = 224..352 a rank (256 global experts, 42..67 rows an expert on average): 181-183 us while
-// the largest expert fits 64 rows, 230-241 us once it does not, against 224-232 us on WIDE.
-// Auto schedules only (an engine set by the caller keeps its kernels); above 16 x 64 tasks an
-// expert the bound selects WIDE directly (no launches that return at once).
-constexpr int kEagerDualMinLargest = kStreamRows + 1;
+// 128 rows (the STREAM engine, an expert of 65..128 rows as two 64-row chunks), WIDE from 129.
+// Measured (whole eager layer) at T = 256..576 a rank (256 global experts, top-6): 235-261 us
+// on the 8-wave kernels with the 128-row STREAM bound, 273-290 us on WIDE; at T = 640 (largest
+// expert 140 rows) WIDE 292 us, the 8-wave kernels with a 192-row bound 320 us.
+// Auto schedules only (an engine set by the caller keeps its kernels); from 8 x 128 tasks an
+// expert (an EP share of 1/8 then routes 128 rows an expert on average, so some expert has
+// more) the bound selects WIDE directly (no launches that return at once).
+constexpr int kEagerDualMinLargest = kStreamAutoMaxRows + 1;
 int gemm_eager_dual_min_largest() { return kEagerDualMinLargest; }
 bool gemm_eager_dual(const GemmArgs& g, int max_rows) {
   return g.engine == GemmEngine::kAuto && gemm_wide_selected(g, max_rows) &&
-         static_cast<int64_t>(max_rows) < 16ll * kStreamRows * g.num_experts;
+         static_cast<int64_t>(max_rows) < 8ll * kStreamAutoMaxRows * g.num_experts;
 }
 
 // The decode pipeline needs the streaming engine's full-chunk shapes for both GEMMs (GEMM2's

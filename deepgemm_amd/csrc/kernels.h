@@ -47,8 +47,8 @@ inline int64_t route_count_ints(int64_t max_tasks, int num_experts) {
   return (chunks > 0 ? chunks : 1) * num_experts * (1 + kRouteWaves);
 }
 
-// Per-expert tile engine of the grouped GEMM: kAuto picks STREAM for experts with <= 64 rows
-// (weight streaming, decode) and TILE otherwise (256x256 MFMA tiles, prefill).
+// Per-expert tile engine of the grouped GEMM: kAuto picks STREAM for experts with <= 128 rows
+// (weight streaming in 64-row chunks, decode) and TILE otherwise (256x256 MFMA tiles, prefill).
 enum class GemmEngine : int { kAuto = 0, kStream = 1, kTile = 2 };
 
 // Fused GEMM1 epilogue: SwiGLU x route weight -> bf16 y.
@@ -137,7 +137,7 @@ int gemm_wide_min_rows(int num_experts);
 // Eager calls on the auto schedule: true when the row bound selects WIDE but the routed rows
 // should choose on the device (a dual launch with rows_on_device = the routing's meta[4], the
 // largest expert's row count, and dual_min_rows = gemm_eager_dual_min_largest: WIDE once an
-// expert has more than 64 rows).
+// expert has more than 128 rows).
 bool gemm_eager_dual(const GemmArgs& g, int max_rows);
 int gemm_eager_dual_min_largest();
 bool gemm_shape_supported(int n, int k);

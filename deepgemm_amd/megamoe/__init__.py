@@ -167,7 +167,7 @@ def get_mega_moe_hip_build_config():
     config["large_opt_3stage_threshold_env"] = _LARGE_OPT_THRESHOLD_ENV
     config["large_opt_3stage_default_threshold"] = _LARGE_OPT_DEFAULT_THRESHOLD
     config["large_opt_3stage_shape"] = "single GPU: experts<=256, topk<=16, H,I % 128 == 0"
-    config["large_opt_3stage_selection"] = ("auto: per expert on device (<=64 rows: streaming "
+    config["large_opt_3stage_selection"] = ("auto: per expert on device (<=128 rows: streaming "
                                             "engine, else 256x256 MFMA tiles); every GEMM on "
                                             "the 4-wave 256x256 kernel when S*K > 8192 and "
                                             ">= 256 rows per expert on average")

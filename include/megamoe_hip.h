@@ -51,7 +51,7 @@ extern "C" {
 
 /* Schedule of mmoe_forward (the reference's MEGAMOE_DCU_USE_LARGE_OPT_3STAGE auto/off/force).
  * The grouped GEMMs have two tile engines; AUTO picks one per expert on the device from its
- * routed row count (<= 64 rows: weight-streaming engine; more: 256x256 MFMA tile engine). When
+ * routed row count (<= 128 rows: weight-streaming engine; more: 256x256 MFMA tile engine). When
  * every expert has many rows (S*K > 8192 and at least 256 rows per expert on average), AUTO
  * and STAGED run both GEMMs on a 4-wave 256x256 kernel instead. */
 #define MMOE_SCHEDULE_AUTO 0       /* per-expert choice on the device */

@@ -273,15 +273,17 @@ FULL_SHAPE_CASES = {
     "clamp10": (96, None, 10.0, "8wave"),
     "wide_2048": (2048, None, None, "wide"),
     # eager calls whose task bound selects WIDE by a small margin: the routing's largest expert
-    # row count chooses on the device (an EP share of 2048 tokens: 1555 rows, at most 63 an
-    # expert -> the 8-wave kernels; of 2304: 1697 rows, 53 an expert on average but 68 in the
-    # largest -> WIDE; of 4096: 3046 rows -> WIDE)
+    # row count chooses on the device, the 8-wave kernels up to 128 rows (an EP share of 2048
+    # tokens: 1555 rows, at most 63 an expert, one STREAM chunk each; of 2304: 1697 rows, 68 in
+    # the largest, two chunks for it; of 4096: 3046 rows, 65..117 rows in every expert), WIDE
+    # above (of 5120: 3858 rows, 144 in the largest)
     "ep_2048": (2048, 256, None, "8wave"),
-    "ep_2304": (2304, 256, None, "wide"),
-    "ep_4096": (4096, 256, None, "wide"),
+    "ep_2304": (2304, 256, None, "8wave"),
+    "ep_4096": (4096, 256, None, "8wave"),
+    "ep_5120": (5120, 256, None, "wide"),
     # clamp 1.0 binds on both sides of the gate and of the up value (h ~ N(0, 1)): the 8-wave
     # epilogue on the STREAM engine (c1 routing), on the TILE engine (Zipf: experts with more
-    # than 64 rows), and the WIDE kernel's requant from h
+    # than 128 rows), and the WIDE kernel's requant from h
     "clamp1_stream": (1024, 256, 1.0, "8wave"),
     "clamp1_tile": (600, "zipf", 1.0, "8wave"),
     "clamp1_wide": (2048, None, 1.0, "wide"),
@@ -299,6 +301,14 @@ def _assert_clamp_binds(h: torch.Tensor, clamp: float, min_frac: float = 0.05):
     log(f"  clamp {clamp}: fractions beyond it {fracs}")
     for k, v in fracs.items():
         assert v >= min_frac, f"clamp does not bind: {k} on {v:.3f} of the values"
+
+
+def _assert_every_engine(counts):
+    """The auto schedule's three per-expert cases occur: STREAM in one 64-row chunk (1..64
+    rows), STREAM in two chunks (65..128) and TILE (more than 128)."""
+    assert ((counts > 0) & (counts <= 64)).any()
+    assert ((counts > 64) & (counts <= 128)).any()
+    assert (counts > 128).any()
 
 
 @pytest.mark.parametrize("case", list(FULL_SHAPE_CASES))
@@ -323,8 +333,8 @@ def test_layer_full_shape(mm, cuda, full_weights, case):
         assert buf.scratch_view("meta")[4].item() == int(tr.routing.counts.max())
     if clamp is not None and clamp < 5.0:
         _assert_clamp_binds(tr.h, clamp)
-    if g == "zipf":  # the TILE engine: experts with more than 64 rows next to small ones
-        assert (tr.routing.counts > 64).any() and ((tr.routing.counts > 0) & (tr.routing.counts <= 64)).any()
+    if g == "zipf":  # the TILE engine (more than 128 rows) next to one- and two-chunk STREAM experts
+        _assert_every_engine(tr.routing.counts)
     _stage_checks(buf, tr, s, clamp)
     _combine_bitwise(mm, buf, y, l1, l2, s, clamp)
     d = O.calc_diff(y.cpu(), tr.y)
@@ -349,8 +359,7 @@ def test_layer_every_schedule_matches_oracle_and_is_deterministic(mm, cuda, full
     torch.cuda.synchronize()
     assert torch.equal(y1, y2)
     tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, unpacked_weights=unpacked)
-    counts = tr.routing.counts
-    assert (counts > 64).any() and ((counts > 0) & (counts <= 64)).any()
+    _assert_every_engine(tr.routing.counts)
     d = O.calc_diff(y1.cpu(), tr.y)
     log(f"  calc_diff={d:.3e}")
     assert d <= CALC_DIFF_BAR
@@ -359,9 +368,10 @@ def test_layer_every_schedule_matches_oracle_and_is_deterministic(mm, cuda, full
 @pytest.mark.parametrize("mode,wide", [("auto", False), ("1", True), ("0", False)])
 def test_eager_dual_applies_to_the_auto_schedule_only(mm, cuda, full_weights, monkeypatch, mode, wide):
     """An EP share of 2048 tokens (1555 routed rows, at most 63 an expert; the task bound selects
-    WIDE): the auto schedule's dual launch lets the routing choose the 8-wave kernels, while a
-    caller-set engine keeps the host's choice -- WIDE for the tile engine (=1), the streaming
-    engine for =0 (which never selects WIDE). Each meets the bar against the oracle."""
+    WIDE): the auto schedule's dual launch lets the routing choose the 8-wave kernels (every
+    expert within the streaming engine's 128 rows), while a caller-set engine keeps the host's
+    choice -- WIDE for the tile engine (=1), the streaming engine for =0 (which never selects
+    WIDE). Each meets the bar against the oracle."""
     l1, l2, l1c, l2c, unpacked = full_weights
     s = 2048
     x_fp8, x_sf, idx, w = make_tokens(s, 4096, 32, 6, seed=1234 + s, global_experts=256)
@@ -373,7 +383,7 @@ def test_eager_dual_applies_to_the_auto_schedule_only(mm, cuda, full_weights, mo
     meta = buf.scratch_view("meta")
     assert (meta[1].item() == 1) == wide, "WIDE GEMM1 exactly when expected"
     tr = O.mega_moe_forward(x_fp8, x_sf, idx, w, l1c, l2c, unpacked_weights=unpacked)
-    assert int(tr.routing.counts.max()) <= 64
+    assert int(tr.routing.counts.max()) <= 128
     d = O.calc_diff(y.cpu(), tr.y)
     log(f"  calc_diff={d:.3e}")
     assert d <= CALC_DIFF_BAR
