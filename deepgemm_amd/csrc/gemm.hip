@@ -1287,7 +1287,6 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
     __syncthreads();
   }
   const int total = s_prefix[E];
-  const int stream_nb = stream_blocks(g);
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
   const bool fast1 = !kAnyK || g.k % (kAChunk / 32) == 0;
   const bool fast2 = !kAnyK || g.k % (kAChunk / 64) == 0;
@@ -1317,8 +1316,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
       tile_tile<kGather, kSwiglu>(g, rs, e, off_e + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM),
                                   nb, smem, s_tt);
     } else {
-      const int mc = local / stream_nb;
-      const int nb = local - mc * stream_nb;
+      // An expert's row chunks of one column block are neighbouring items, so they run in the
+      // same round on the same XCD and read those weight columns from HBM once (through L2),
+      // wherever the XCD ranges and rounds cut the item list.
+      const int nch = (cnt + kStreamRows - 1) / kStreamRows;
+      const int nb = local / nch;
+      const int mc = local - nb * nch;
       const int mrows = min(kStreamRows, cnt - mc * kStreamRows);
       const int row0 = off_e + mc * kStreamRows;
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
