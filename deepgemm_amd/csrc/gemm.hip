@@ -24,9 +24,9 @@
 // Two persistent kernels per GEMM; the host picks one (gemm_wide_selected):
 //  * the 8-wave kernel (one workgroup per CU) runs two tile engines, each expert's chosen on
 //    the device from its routed row count, and can route the tasks itself (decode sizes):
-//    - STREAM engine (<= 128 rows on the auto schedule: decode, HBM-bound on the weights;
-//      an expert with more than 64 rows is two row chunks). A workgroup tile is
-//      (expert, 512 output columns, <= 64 rows) over the full K; wave w owns columns
+//    - STREAM engine (<= 128 rows on the auto schedule: decode, HBM-bound on the weights).
+//      A workgroup tile is (expert, 512 output columns, <= 128 rows: 1, 2 or 4 row tiles of
+//      32) over the full K; wave w owns columns
 //      [64w, 64w + 64) and streams its weight columns from global memory into a register ring
 //      4 steps deep (Marlin gives each lane 16 contiguous k-bytes of one weight row; 16 lanes
 //      read 256 contiguous bytes), with no barrier: B never touches LDS. The A rows, the same
@@ -59,8 +59,9 @@ constexpr int kGemmWaves = kGemmThreads / kWave;
 constexpr int kMaxGemmExperts = 256;
 // STREAM engine
 constexpr int kStreamUnit = 64;     // output columns per wave
-constexpr int kStreamRows = 64;     // rows per workgroup tile
-constexpr int kStreamAutoMaxRows = 128;  // the auto schedule streams experts up to this many rows
+constexpr int kStreamRows = 64;     // rows of a decode pipeline group
+constexpr int kStreamItemRows = 128;  // rows of a STREAM item of the 8-wave GEMM kernel
+constexpr int kStreamAutoMaxRows = kStreamItemRows;  // the auto schedule streams experts up to this
 constexpr int kStreamDepth = 4;     // 64-k weight steps in flight per wave
 constexpr int kAChunk = 65536;      // bytes of one A chunk buffer (32*MT rows x 2048/MT k)
 constexpr int kALoads = kAChunk / 1024 / kGemmWaves;  // 16-byte A loads per lane per chunk
@@ -197,7 +198,7 @@ __device__ __forceinline__ void publish_tile_scales(TileTables& tt, const TileSc
 }
 
 // Stores a wave's MT x (32 rows) x 64 columns of accumulators: rows [row0, row0 + mrows) of
-// the output (mrows <= 64; table row trow0 + r holds row r's scales), 64-column unit `unit`
+// the output (mrows <= 32 * MT; table row trow0 + r holds row r's scales), 64-column unit `unit`
 // of the output (SwiGLU: 32 channels).
 // kCoherent: the stores go out device-coherent (sc1, written through the XCD's L2): GEMM2's
 // partial rows, so that workgroups of other XCDs can read them in the same launch, and GEMM1's
@@ -287,8 +288,9 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ int swizzle_piece(int p, int r) { return (p & ~7) | ((p ^ r) & 7); }
 
 // One workgroup tile (expert e, 512-column block nb, rows [row0, row0 + mrows), mrows <= 32*MT)
-// over the full K. kFast: K is a multiple of the chunk (2048/MT k), ring 4 steps deep; else
-// 128-k chunks and a one-step ring (small shapes).
+// over the full K. kFast: K is a multiple of the chunk (2048/MT k), ring 4 steps deep (2 for
+// four row tiles, whose 128 accumulators leave no room for more); else 128-k chunks and a
+// one-step ring (small shapes).
 //
 // A chunk c+1 is loaded into registers (8 x 16 bytes per lane, whole 128-byte lines: lane l of
 // load i covers LDS bytes gi*1024 + 16*l of the chunk buffer, gi = 8i + wave) right after the
@@ -309,7 +311,8 @@ template <bool kGather, bool kSwiglu, int MT, bool kFast, bool kEarly = false, b
 __device__ void stream_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
                             uint8_t* smem, TileTables& tt, const Hook& before_a = Hook{}) {
   static_assert(!kAResident || (kEarly && kFast), "a resident A is staged by the hook");
-  constexpr int D = kFast ? kStreamDepth : 1;
+  // four row tiles: the accumulators take the registers of two ring steps
+  constexpr int D = kFast ? (MT == 4 ? kStreamDepth / 2 : kStreamDepth) : 1;
   constexpr int kFullChunk = kAChunk / (32 * MT);  // k-bytes per chunk
   const int kc = kFast ? kFullChunk : 128;
   const int spc = kc / 64;  // steps per chunk
@@ -1125,7 +1128,7 @@ __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const 
         const bool tile = all_tile || g.engine == GemmEngine::kTile ||
                           (g.engine == GemmEngine::kAuto && cnt > kStreamAutoMaxRows);
         items = tile ? (cnt + tile_rows - 1) / tile_rows * tile_nb
-                     : (cnt + kStreamRows - 1) / kStreamRows * stream_nb;
+                     : (cnt + kStreamItemRows - 1) / kStreamItemRows * stream_nb;
         s_tile[e] = tile;
       }
       const int inc = wave_inclusive_sum(items);
@@ -1290,6 +1293,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
   const bool fast1 = !kAnyK || g.k % (kAChunk / 32) == 0;
   const bool fast2 = !kAnyK || g.k % (kAChunk / 64) == 0;
+  const bool fast4 = !kAnyK || g.k % (kAChunk / 128) == 0;
   const ItemDeal deal = deal_items(total);
   // the route weights cached in LDS are valid until the first item's loads overwrite them
   const float* task_w = reinterpret_cast<const float*>(smem);
@@ -1316,22 +1320,25 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmArgs 
       tile_tile<kGather, kSwiglu>(g, rs, e, off_e + mt * kTileBM, min(kTileBM, cnt - mt * kTileBM),
                                   nb, smem, s_tt);
     } else {
-      // An expert's row chunks of one column block are neighbouring items, so they run in the
-      // same round on the same XCD and read those weight columns from HBM once (through L2),
-      // wherever the XCD ranges and rounds cut the item list.
-      const int nch = (cnt + kStreamRows - 1) / kStreamRows;
+      // An expert's row chunks of one column block (more than one only on the streaming
+      // schedule) are neighbouring items, so they run in the same round on the same XCD and
+      // read those weight columns from HBM once (through L2).
+      const int nch = (cnt + kStreamItemRows - 1) / kStreamItemRows;
       const int nb = local / nch;
       const int mc = local - nb * nch;
-      const int mrows = min(kStreamRows, cnt - mc * kStreamRows);
-      const int row0 = off_e + mc * kStreamRows;
+      const int mrows = min(kStreamItemRows, cnt - mc * kStreamItemRows);
+      const int row0 = off_e + mc * kStreamItemRows;
       RowSrc rs{g.row_token, g.sw.row_weight, 0};
       if (fused) {
-        const int r0 = mc * kStreamRows;
+        const int r0 = mc * kStreamItemRows;
         fused_rows(ra, ntasks, e, cnt, off_e, s_wcnt, s_ev, item_task_w, r0,
-                   nb == 0 ? r0 : 0, nb == 0 ? r0 + kStreamRows : 0, 0, 0, s_task, s_tok, s_rw);
+                   nb == 0 ? r0 : 0, nb == 0 ? r0 + kStreamItemRows : 0, 0, 0, s_task, s_tok, s_rw);
         rs = RowSrc{s_tok, s_rw, row0};
       }
-      if (mrows > 32) {
+      if (mrows > 64) {
+        if (fast4) stream_tile<kGather, kSwiglu, 4, true>(g, rs, e, row0, mrows, nb, smem, s_tt);
+        else if (kAnyK) stream_tile<kGather, kSwiglu, 4, false>(g, rs, e, row0, mrows, nb, smem, s_tt);
+      } else if (mrows > 32) {
         if (fast2) stream_tile<kGather, kSwiglu, 2, true>(g, rs, e, row0, mrows, nb, smem, s_tt);
         else if (kAnyK) stream_tile<kGather, kSwiglu, 2, false>(g, rs, e, row0, mrows, nb, smem, s_tt);
       } else {
@@ -1926,7 +1933,7 @@ hipError_t launch_engines_k(const GemmArgs& g, int max_rows, int num_cus, hipStr
   }
   // upper bound of the work items over any split of max_rows rows into the experts
   const int64_t stream_nb = (g.n / kStreamUnit + kGemmWaves - 1) / kGemmWaves;
-  const int64_t stream_items = (static_cast<int64_t>(max_rows) / kStreamRows + g.num_experts) * stream_nb;
+  const int64_t stream_items = (static_cast<int64_t>(max_rows) / kStreamItemRows + g.num_experts) * stream_nb;
   const int64_t tile_items =
       (static_cast<int64_t>(max_rows) / kTileBM + g.num_experts) * ((g.n + kTileBN - 1) / kTileBN);
   const int64_t bound = g.engine == GemmEngine::kStream ? stream_items
@@ -1976,10 +1983,11 @@ int gemm_wide_min_rows(int num_experts) {
 // Eager calls whose row bound selects WIDE only by a small margin: the routed rows may be far
 // fewer (an EP share keeps ~1/8 of its slots), so both kernels go out and the routing's largest
 // expert row count chooses on the device -- the 8-wave kernels while every expert has at most
-// 128 rows (the STREAM engine, an expert of 65..128 rows as two 64-row chunks), WIDE from 129.
-// Measured (whole eager layer) at T = 256..576 a rank (256 global experts, top-6): 235-261 us
-// on the 8-wave kernels with the 128-row STREAM bound, 273-290 us on WIDE; at T = 640 (largest
-// expert 140 rows) WIDE 292 us, the 8-wave kernels with a 192-row bound 320 us.
+// 128 rows (one STREAM item a column block), WIDE from 129.
+// Measured (whole eager layer, cold caches) at T = 256..576 a rank (256 global experts, top-6):
+// 192-209 us on the 8-wave kernels (one 128-row item per expert and column block: 256 items,
+// one round), 273-290 us on WIDE. Above, streaming experts of up to 256 rows (two items) and
+// going WIDE only past that was within -4..+3% of this choice at T = 640..1024 (279-327 us).
 // Auto schedules only (an engine set by the caller keeps its kernels); from 8 x 128 tasks an
 // expert (an EP share of 1/8 then routes 128 rows an expert on average, so some expert has
 // more) the bound selects WIDE directly (no launches that return at once).

@@ -48,7 +48,7 @@ inline int64_t route_count_ints(int64_t max_tasks, int num_experts) {
 }
 
 // Per-expert tile engine of the grouped GEMM: kAuto picks STREAM for experts with <= 128 rows
-// (weight streaming in 64-row chunks, decode) and TILE otherwise (256x256 MFMA tiles, prefill).
+// (weight streaming, decode) and TILE otherwise (256x256 MFMA tiles, prefill).
 enum class GemmEngine : int { kAuto = 0, kStream = 1, kTile = 2 };
 
 // Fused GEMM1 epilogue: SwiGLU x route weight -> bf16 y.
