@@ -51,6 +51,13 @@ CONFIGS = {
                workload="c3 prefill T=32768: 8x32768 source tokens, top-6 of 256, 0-31 kept"),
     "c4": dict(id=4, tokens=8192, global_experts=None, routing="zipf", cpu_reps=1,
                workload="c4 skew T=8192: top-6 i.i.d. Zipf(1.2) over 28 experts, 4 empty"),
+    # EP shares between c1 and c2 (not BASELINE configs; run only when named in --configs):
+    # T=448 puts at most 128 rows on an expert (the 8-wave kernels' 128-row STREAM items), T=1024
+    # one WIDE row block an expert
+    "m1": dict(id=5, tokens=3584, global_experts=256, routing="softmax", cpu_reps=1,
+               workload="m1 EP share T=448: 8x448 source tokens, top-6 of 256, 0-31 kept"),
+    "m2": dict(id=6, tokens=8192, global_experts=256, routing="softmax", cpu_reps=1,
+               workload="m2 EP share T=1024: 8x1024 source tokens, top-6 of 256, 0-31 kept"),
 }
 HEADLINE = "c1"
 
@@ -65,7 +72,9 @@ def algorithmic_bytes(rows: int, touched: int) -> dict:
     h, i = HIDDEN, INTER
     layer = (touched * (2 * i * h + h * i) + touched * (2 * i + h) * 4 + rows * (h + 4)
              + rows * (i + 4) * 2 + rows * h * 2)
-    gemm1 = touched * 2 * i * h + touched * 2 * i * 4 + rows * (h + 4) + rows * 2 * i * 2
+    # GEMM1 applies the SwiGLU x route weight in its epilogue: it writes y [R, I] in bf16 (the
+    # reference's fused output), not h [R, 2I]
+    gemm1 = touched * 2 * i * h + touched * 2 * i * 4 + rows * (h + 4) + rows * i * 2
     gemm2 = touched * h * i + touched * h * 4 + rows * (i + 4) + rows * h * 2
     # the decode pipeline runs the whole layer (routing through the combine) in one launch
     return dict(layer=layer, gemm1=gemm1, gemm2=gemm2, pipeline=layer)
