@@ -67,6 +67,10 @@ ROUTE_CASES = {
     "zipf": (3000, 32, 6, "zipf"),
     "wide": (2500, 40, 8, 64),
     "chunked": (20000, 32, 6, 256),  # 120,000 tasks: count + scatter kernels over 117 chunks
+    # just past the one-workgroup kernel (16,384 tasks): 17 chunks, the last of 2 tasks; 32 full
+    # chunks over 256 experts
+    "chunks_ragged": (2731, 32, 6, 256),
+    "chunks_e256": (4096, 256, 8, None),
 }
 
 
