@@ -195,6 +195,9 @@ def _combine_bitwise(mm, buf, y, l1, l2, s, clamp):
     (1500, 5, 768, 256, 6, 8, None),
     # >= 16 tokens a CU: the whole-row combine; most tokens have one routed slot (direct rows)
     (4500, 4, 256, 256, 2, 16, None),
+    # ~100 rows an expert: one 128-row STREAM item (4 row tiles) a column block, with K not a
+    # multiple of the 512-byte chunk in both GEMMs (128-k chunks, one-step ring)
+    (100, 4, 640, 384, 4, None, None),
     # GEMM1's in-kernel routing over more than one 64-expert scan chunk (S*K <= 8192), up to
     # its largest expert count (255: expert ids in a byte)
     (512, 160, 256, 128, 8, None, None),
