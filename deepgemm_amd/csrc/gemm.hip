@@ -44,7 +44,6 @@
 //    registers and only A through LDS; described at wide_tile.
 #include <algorithm>
 #include <atomic>
-#include <type_traits>
 
 #include "common.cuh"
 #include "kernels.h"
@@ -792,10 +791,7 @@ __device__ __forceinline__ void store_wide_swiglu(const GemmArgs& g, const v16f 
 
 // TM row tiles of 32: BM/32 for a full tile; fewer (4, 2 or 1) for an expert's last tile of
 // at most 128, 64 or 32 rows (a fraction of the MFMAs and A traffic for the row remainder).
-// kOnce: the expert has this one row block, so no other tile reads these weight columns and
-// they are streamed with the nontemporal hint (where row blocks share them through L2, the
-// plain loads keep them there).
-template <bool kGather, bool kSwiglu, int BM, int TM, bool kOnce = false, typename Hook = NoHook>
+template <bool kGather, bool kSwiglu, int BM, int TM, typename Hook = NoHook>
 __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, int mrows, int nb,
                           uint8_t* smem, const Hook& before_epilogue = Hook{}) {
   using W = WideShape<BM>;
@@ -861,13 +857,8 @@ __device__ void wide_tile(const GemmArgs& g, const RowSrc& rs, int e, int row0, 
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       const uint8_t* q = bp[tn] + static_cast<int64_t>(s) * 1024;
-      if constexpr (kOnce) {
-        br[slot][tn][0] = ld16_stream(q);
-        br[slot][tn][1] = ld16_stream(q + 256);
-      } else {
-        br[slot][tn][0] = ld16(q);
-        br[slot][tn][1] = ld16(q + 256);
-      }
+      br[slot][tn][0] = ld16(q);
+      br[slot][tn][1] = ld16(q + 256);
     }
   };
 
@@ -1798,17 +1789,6 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
   const int total = s_prefix[E];
   const int tile_nb = (g.n + kTileBN - 1) / kTileBN;
   const RowSrc rs{g.row_token, g.sw.row_weight, 0};
-  auto run_tile = [&](auto once_c, int e, int row0, int mrows, int nb, const auto& before_epilogue) {
-    constexpr bool kOnce = decltype(once_c)::value;
-    if (BM == 256 && mrows > 128)
-      wide_tile<kGather, kSwiglu, BM, (BM == 256 ? 8 : 4), kOnce>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
-    else if (mrows > 64)
-      wide_tile<kGather, kSwiglu, BM, 4, kOnce>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
-    else if (mrows > 32)
-      wide_tile<kGather, kSwiglu, BM, 2, kOnce>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
-    else
-      wide_tile<kGather, kSwiglu, BM, 1, kOnce>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
-  };
   auto run_item = [&](int t, const auto& before_epilogue) {
     const int e = expert_of_item(s_prefix, E, t);
     const int cnt = s_count[e];
@@ -1816,10 +1796,14 @@ __global__ __launch_bounds__(kWideThreads, WideShape<BM>::kWavesPerSimd) void wi
     tile_coords(t - s_prefix[e], cnt, tile_nb, mt, nb, BM);
     const int mrows = min(BM, cnt - mt * BM);
     const int row0 = s_off[e] + mt * BM;
-    if (cnt <= BM)
-      run_tile(std::true_type{}, e, row0, mrows, nb, before_epilogue);
+    if (BM == 256 && mrows > 128)
+      wide_tile<kGather, kSwiglu, BM, (BM == 256 ? 8 : 4)>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
+    else if (mrows > 64)
+      wide_tile<kGather, kSwiglu, BM, 4>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
+    else if (mrows > 32)
+      wide_tile<kGather, kSwiglu, BM, 2>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
     else
-      run_tile(std::false_type{}, e, row0, mrows, nb, before_epilogue);
+      wide_tile<kGather, kSwiglu, BM, 1>(g, rs, e, row0, mrows, nb, smem, before_epilogue);
   };
   // One item at a time from the static deal or from the claims. Claiming only pays when a
   // workgroup has few items (the last round's granularity is then a large share of its work;
@@ -2000,10 +1984,10 @@ int gemm_wide_min_rows(int num_experts) {
 // fewer (an EP share keeps ~1/8 of its slots), so both kernels go out and the routing's largest
 // expert row count chooses on the device -- the 8-wave kernels while every expert has at most
 // 128 rows (one STREAM item a column block), WIDE from 129.
-// Measured (whole eager layer, cold caches) at T = 256..576 a rank (256 global experts, top-6):
-// 192-209 us on the 8-wave kernels (one 128-row item per expert and column block: 256 items,
-// one round), 273-290 us on WIDE. Above, streaming experts of up to 256 rows (two items) and
-// going WIDE only past that was within -4..+3% of this choice at T = 640..1024 (279-327 us).
+// Measured (whole eager layers after a read-only cache flush) at T = 256..576 a rank (256 global
+// experts, top-6): 188-202 us on the 8-wave kernels (one 128-row item per expert and column
+// block: 256 items, one round) against 230-248 us on WIDE. Streaming experts of up to 256 rows
+// (two items) and going WIDE only past that was within -4..+3% of this choice at T = 640..1024.
 // Auto schedules only (an engine set by the caller keeps its kernels); from 8 x 128 tasks an
 // expert (an EP share of 1/8 then routes 128 rows an expert on average, so some expert has
 // more) the bound selects WIDE directly (no launches that return at once).
