@@ -94,6 +94,31 @@ def test_static_scratch_wide_path(mm, cuda):
         assert torch.equal(y_got.view(torch.int16), y_ref.view(torch.int16)), f"S={s}"
 
 
+def test_static_scratch_stream_items(mm, cuda):
+    """Top-8 over an expert width of 1536 (GEMM2's K keeps it off the one-launch pipeline): the
+    8-wave kernels route in-kernel and stream every expert, those above 64 rows as one 128-row
+    item a column block; twice in a row, the second call smaller, bitwise equal to
+    mmoe_forward."""
+    e, hdim, inter, k = 32, 4096, 1536, 8
+    l1, l2 = make_weights_gpu(e, hdim, inter, seed=4323, mm=mm)
+    for s in (1024, 512):
+        log(f"static scratch, 8-wave STREAM items: S={s}")
+        x_fp8, x_sf, idx, w = make_tokens(s, hdim, e, k, seed=55 + s, global_experts=128)
+        buf = mm.get_symm_buffer_for_mega_moe(None, e, s, k, hdim, inter)
+        _load(buf, x_fp8, x_sf, idx, w)
+        y_ref = torch.empty((s, hdim), dtype=torch.bfloat16, device=cuda)
+        mm.fp8_w8a8_mega_moe(y_ref, l1, l2, buf)
+        torch.cuda.synchronize()
+        assert buf.scratch_view("meta")[1].item() == 0, "the 8-wave GEMM1 ran"
+        if s == 1024:
+            assert int(buf.scratch_view("counts").max()) > 64, "an expert on a 128-row item"
+        y_got = torch.full((s, hdim), 7.0, dtype=torch.bfloat16, device=cuda)
+        st = _static_call(mm, y_got, l1, l2, buf)
+        assert st == 0, mm._capi.status_string(st)
+        torch.cuda.synchronize()
+        assert torch.equal(y_got.view(torch.int16), y_ref.view(torch.int16)), f"S={s}"
+
+
 def test_static_scratch_limit_is_refused(mm, cuda):
     """A capacity whose scratch exceeds MMOE_STATIC_SCRATCH_BYTES returns
     MMOE_ERR_STATIC_SCRATCH before any launch."""
