@@ -1110,8 +1110,8 @@ __device__ __forceinline__ int stream_blocks(const GemmArgs& g) {
 
 // Wave 0 fills s_prefix[0..E] with the exclusive prefix of the workgroup work items of the
 // experts and s_tile[e] with the expert's engine (1 = TILE), from the routed rows s_count[e].
-// A STREAM item is one (64-row chunk, 512-column block); a TILE item is one 256 x 256 tile
-// (row-block major).
+// A STREAM item is one (128-row chunk, 512-column block), an expert's chunks of one column
+// block next to each other; a TILE item is one 256 x 256 tile (tile_coords' order).
 __device__ void plan_items(const GemmArgs& g, int* s_prefix, int* s_tile, const int* s_count,
                            bool all_tile = false, int tile_rows = kTileBM) {
   const int E = g.num_experts;
