@@ -994,6 +994,49 @@ def _sampled_oracle_check(mm, buf, n, y, x_fp8, x_sf, idx, w, l1c, l2c, unpacked
     return ref
 
 
+def test_graph_ep_share_mid_bucket(mm, cuda, full_weights):
+    """An EP share between the decode and prefill buckets (5120 tokens a rank, 256 global
+    experts: its bound selects WIDE, ~3.9K routed rows): every replay below 8193 routed rows runs
+    the 8-wave kernels of the dual launch -- 128-row STREAM items, the TILE engine for the few
+    experts above 128 rows -- and 1365 tokens (8190 tasks) route in GEMM1 itself. Each replay
+    matches the oracle on its prefix, is bitwise equal to an eager call on it where that call
+    ran the same GEMM1 kernel, and leaves the rows past it alone."""
+    l1, l2, l1c, l2c, unpacked = full_weights
+    s_max = 5120
+    x_fp8, x_sf, idx, w = make_tokens(s_max, 4096, 32, 6, seed=1234 + s_max, global_experts=256)
+    buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    _load_bucket(buf, x_fp8, x_sf, idx, w)
+    y = torch.zeros((s_max, 4096), dtype=torch.bfloat16, device=cuda)
+    log("mid EP-share graph: warm-up and capture at 5120 tokens")
+    graph = _capture_bucket(mm, y, l1, l2, buf, "stages_fused_cuda_graph")
+    ref_buf = mm.get_symm_buffer_for_mega_moe(None, 32, s_max, 6, 4096, 2048)
+    bitwise = 0
+    largest_full = 0
+    for n in (s_max, 3584, 2000, 1365):
+        tr = O.mega_moe_forward(x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1c, l2c, unpacked_weights=unpacked)
+        assert tr.routing.num_rows < 8193
+        largest_full = max(largest_full, int(tr.routing.counts.max()))
+        y_ref = run_layer(mm, ref_buf, x_fp8[:n], x_sf[:n], idx[:n], w[:n], l1, l2)
+        torch.cuda.synchronize()
+        ref_wide = bool(ref_buf.scratch_view("meta")[1].item() == 1)
+        for rep in range(2):
+            log(f"  replay {rep} with runtime tokens={n}")
+            y.fill_(7.0)
+            buf.cuda_graph_num_tokens.fill_(n)
+            graph.replay()
+            torch.cuda.synchronize()
+            meta = buf.scratch_view("meta").cpu()
+            assert int(meta[0]) == tr.routing.num_rows and int(meta[3]) == 0, f"n={n}"
+            assert int(meta[1]) == 0, f"n={n}: the 8-wave GEMM1 ran"
+            _oracle_prefix_check(buf, n, tr, y, unpacked)
+            if not ref_wide:
+                assert torch.equal(y[:n].view(torch.int16), y_ref.view(torch.int16)), f"replay n={n}"
+                bitwise += 1
+            assert torch.all(y[n:] == 7.0), f"rows past the prefix were written (n={n})"
+    assert bitwise > 0
+    assert largest_full > 128, "an expert on the TILE engine in the full replay"
+
+
 def test_graph_ep_share_zero_rows(mm, cuda, full_weights):
     """An EP share (256 global experts, ~45% of the tokens without a local slot) in a
     65536-token bucket (~49K routed rows: 14 WIDE tiles a workgroup, the static deal): a full
